@@ -1,0 +1,117 @@
+/*
+ * tinyinfer_mxfp4.h -- C ABI of the MI355X (gfx950) MXFP4 weight-only MLP.
+ *
+ * Plain pointers and sizes only. Every pointer is a device pointer on the
+ * current HIP device unless stated otherwise. `stream` is a hipStream_t
+ * passed as void* (NULL = the legacy default stream). Work is enqueued
+ * asynchronously and nothing here synchronizes, except where a function says
+ * it does. Every function returns 0 on success or a TI_* status code, and
+ * never throws.
+ *
+ * Layout (reference tinyinfer/layers/linear.py:36-48,
+ * tinyinfer/quantization/quantize_mxfp4.py:233-253):
+ *   X           [N, hidden]                    bf16 or fp16, row-major
+ *   gate, up    [intermediate, hidden/2]       uint8, e2m1 pairs, low nibble first
+ *   gate_scale,
+ *   up_scale    [intermediate, hidden/32]      uint8 e8m0 (byte = exponent + 127)
+ *   down        [hidden, intermediate/2]       uint8
+ *   down_scale  [hidden, intermediate/32]      uint8
+ *   tmp         [N, intermediate]              activation dtype (SiLU(g)*u)
+ *   O           [N, hidden]                    activation dtype
+ */
+#ifndef TINYINFER_MXFP4_H_
+#define TINYINFER_MXFP4_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define TI_OK 0
+#define TI_ERR_INVALID_ARG 1      /* null pointer, zero/negative size, bad enum */
+#define TI_ERR_BAD_SHAPE 2        /* hidden or intermediate not a multiple of 32 */
+#define TI_ERR_BAD_DTYPE 3        /* dtype code not supported by this entry point */
+#define TI_ERR_HIP 4              /* a HIP runtime call failed (see last HIP error) */
+#define TI_ERR_NO_DEVICE 5        /* no gfx950 device is current */
+#define TI_ERR_TOO_LARGE 6        /* a size exceeds what the kernels index */
+
+/* dtype codes: the reference's dtype_code values (mlp_fp4.cu:481-515), plus fp32. */
+#define TI_DTYPE_F16 0
+#define TI_DTYPE_BF16 1
+#define TI_DTYPE_F32 2
+
+/* Kernel paths for tinyinfer_mlp_forward_mxfp4_path. */
+#define TI_PATH_AUTO 0            /* same choice as tinyinfer_mlp_forward_mxfp4 */
+#define TI_PATH_SKINNY 1          /* dequant skinny-GEMM on MFMA (weights streamed once per 64 tokens) */
+#define TI_PATH_GEMM 2            /* LDS-tiled dequant -> bf16 MFMA GEMM */
+
+/* Quantizer flag bits written to *flags by tinyinfer_mxfp4_quantize. */
+#define TI_QFLAG_NONFINITE 1u     /* NaN/Inf in the input */
+#define TI_QFLAG_EXP_RANGE 2u     /* a block exponent falls outside [-127, 127] */
+
+/*
+ * Fused MXFP4 MLP forward: O = down( SiLU(X gate^T) * (X up^T) ).
+ * Replaces the reference's C entry point
+ *   extern "C" void mlp_forward_mxfp4_cuda(X, gate, gate_scale, up, up_scale,
+ *       down, down_scale, N, hidden_dim, intermediate, tmp, O, dtype_code)
+ *   (tinyinfer/csrc/mlp_fp4.cu:466-518, declared tinyinfer/csrc/bind.cpp:640-654)
+ * with the same arguments in the same order, plus `stream`; errors are
+ * returned instead of thrown. `tmp` must hold N*intermediate elements of the
+ * activation dtype; on return it holds bf16/fp16 SiLU(g)*u, as in the
+ * reference. The kernel path is chosen from N.
+ */
+int tinyinfer_mlp_forward_mxfp4(const void* X, const uint8_t* gate, const uint8_t* gate_scale,
+                                const uint8_t* up, const uint8_t* up_scale, const uint8_t* down,
+                                const uint8_t* down_scale, size_t N, size_t hidden_dim,
+                                size_t intermediate, void* tmp, void* O, int dtype_code,
+                                void* stream);
+
+/*
+ * Same as tinyinfer_mlp_forward_mxfp4 with the kernel path forced
+ * (TI_PATH_*). No reference counterpart: the reference has one path. Used by
+ * parity tests and the benchmark to exercise both kernels at any N.
+ */
+int tinyinfer_mlp_forward_mxfp4_path(const void* X, const uint8_t* gate, const uint8_t* gate_scale,
+                                     const uint8_t* up, const uint8_t* up_scale,
+                                     const uint8_t* down, const uint8_t* down_scale, size_t N,
+                                     size_t hidden_dim, size_t intermediate, void* tmp, void* O,
+                                     int dtype_code, int path, void* stream);
+
+/*
+ * Device dequantization: out[rows, k] = e2m1(packed) * 2^(scale-127), bit-exact.
+ * Replaces dequantize_chunk (tinyinfer/quantization/quantize_mxfp4.py:67-85)
+ * and the device decode helpers decode_e2m1 / decode_e8m0
+ * (tinyinfer/csrc/utils.h:87-127). out_dtype is TI_DTYPE_F32 or TI_DTYPE_BF16
+ * (every value is exact in both). Scale byte 255 yields NaN, as the reference
+ * GPU decode does; the reference CPU decode raises on it instead, and the
+ * Python wrapper does the same.
+ */
+int tinyinfer_mxfp4_dequant(const uint8_t* packed, const uint8_t* scale, size_t rows, size_t k,
+                            void* out, int out_dtype, void* stream);
+
+/*
+ * Device quantization, bit-exact with the reference quantizer:
+ * quantize_chunk (tinyinfer/quantization/quantize_mxfp4.py:28-64).
+ * w[rows, k] in TI_DTYPE_F32 / BF16 / F16 -> packed[rows, k/2], scale[rows, k/32].
+ * `flags` is a device uint32 that the kernel ORs TI_QFLAG_* bits into; this
+ * function clears it first. The caller reads it after the stream completes.
+ * Where the reference raises ValueError, the bytes written for the offending
+ * blocks are unspecified.
+ */
+int tinyinfer_mxfp4_quantize(const void* w, int in_dtype, size_t rows, size_t k, uint8_t* packed,
+                             uint8_t* scale, uint32_t* flags, void* stream);
+
+/* Human-readable text for a TI_* status code (static storage). */
+const char* tinyinfer_mxfp4_status_string(int status);
+
+/* ABI version of this library (increments on any signature change). */
+int tinyinfer_mxfp4_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TINYINFER_MXFP4_H_ */

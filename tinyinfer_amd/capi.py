@@ -1,0 +1,132 @@
+"""ctypes binding of the C ABI (``include/tinyinfer_mxfp4.h``).
+
+This is the binding a non-torch host (or a test) uses: every entry point
+takes raw device pointers, sizes and a stream handle.  ``torch`` tensors are
+accepted by the convenience wrappers only to read ``data_ptr()`` and the
+current stream; nothing crosses the boundary as a torch type.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from functools import lru_cache
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libtinyinfer_mxfp4.so")
+
+TI_OK = 0
+TI_ERR_INVALID_ARG = 1
+TI_ERR_BAD_SHAPE = 2
+TI_ERR_BAD_DTYPE = 3
+TI_ERR_HIP = 4
+TI_ERR_NO_DEVICE = 5
+TI_ERR_TOO_LARGE = 6
+
+TI_DTYPE_F16 = 0
+TI_DTYPE_BF16 = 1
+TI_DTYPE_F32 = 2
+
+TI_PATH_AUTO = 0
+TI_PATH_SKINNY = 1
+TI_PATH_GEMM = 2
+
+TI_QFLAG_NONFINITE = 1
+TI_QFLAG_EXP_RANGE = 2
+
+# name -> (restype, argtypes); mirrors include/tinyinfer_mxfp4.h
+_vp, _u8p, _sz, _int = ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
+SIGNATURES = {
+    "tinyinfer_mlp_forward_mxfp4": (_int, [_vp, _u8p, _u8p, _u8p, _u8p, _u8p, _u8p, _sz, _sz, _sz, _vp, _vp, _int, _vp]),
+    "tinyinfer_mlp_forward_mxfp4_path": (_int, [_vp, _u8p, _u8p, _u8p, _u8p, _u8p, _u8p, _sz, _sz, _sz, _vp, _vp, _int, _int, _vp]),
+    "tinyinfer_mxfp4_dequant": (_int, [_u8p, _u8p, _sz, _sz, _vp, _int, _vp]),
+    "tinyinfer_mxfp4_quantize": (_int, [_vp, _int, _sz, _sz, _u8p, _u8p, _vp, _vp]),
+    "tinyinfer_mxfp4_status_string": (ctypes.c_char_p, [_int]),
+    "tinyinfer_mxfp4_abi_version": (_int, []),
+}
+
+
+class TinyInferError(RuntimeError):
+    def __init__(self, status: int, what: str):
+        self.status = status
+        super().__init__(f"{what} failed: {status_string(status)} (status {status})")
+
+
+@lru_cache(maxsize=1)
+def lib() -> ctypes.CDLL:
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built; run: python -m tinyinfer_amd.build")
+    handle = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = res
+        fn.argtypes = args
+    return handle
+
+
+def status_string(status: int) -> str:
+    return lib().tinyinfer_mxfp4_status_string(int(status)).decode()
+
+
+def _check(status: int, what: str) -> None:
+    if status != TI_OK:
+        raise TinyInferError(status, what)
+
+
+def _stream_handle(stream=None) -> int:
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return int(s.cuda_stream)
+
+
+def _act_code(dtype) -> int:
+    import torch
+    if dtype == torch.bfloat16:
+        return TI_DTYPE_BF16
+    if dtype == torch.float16:
+        return TI_DTYPE_F16
+    raise ValueError("MXFP4 MLP only supports FP16 and BF16 activations")
+
+
+def mlp_forward(x, gp, gs, up, us, dp, ds, out=None, tmp=None, path: int = TI_PATH_AUTO, stream=None):
+    """Run the MLP through the C ABI on torch-owned device buffers.
+
+    ``out``/``tmp`` may be preallocated ([N, hidden] / [N, intermediate] in
+    ``x``'s dtype); they are allocated when omitted.  Returns ``out``."""
+    import torch
+    n, hidden = x.shape
+    inter = gp.shape[0]
+    if out is None:
+        out = torch.empty((n, hidden), dtype=x.dtype, device=x.device)
+    if tmp is None:
+        tmp = torch.empty((n, inter), dtype=x.dtype, device=x.device)
+    st = lib().tinyinfer_mlp_forward_mxfp4_path(
+        x.data_ptr(), gp.data_ptr(), gs.data_ptr(), up.data_ptr(), us.data_ptr(), dp.data_ptr(), ds.data_ptr(),
+        n, hidden, inter, tmp.data_ptr(), out.data_ptr(), _act_code(x.dtype), int(path), _stream_handle(stream))
+    _check(st, "tinyinfer_mlp_forward_mxfp4")
+    return out
+
+
+def dequant(packed, scale, out_dtype=None, stream=None):
+    import torch
+    out_dtype = out_dtype or torch.float32
+    rows, half_k = packed.shape
+    out = torch.empty((rows, 2 * half_k), dtype=out_dtype, device=packed.device)
+    code = TI_DTYPE_F32 if out_dtype == torch.float32 else TI_DTYPE_BF16
+    st = lib().tinyinfer_mxfp4_dequant(packed.data_ptr(), scale.data_ptr(), rows, 2 * half_k, out.data_ptr(),
+                                       code, _stream_handle(stream))
+    _check(st, "tinyinfer_mxfp4_dequant")
+    return out
+
+
+def quantize(w, stream=None):
+    """Device quantizer; returns (packed, scale, flags) device tensors."""
+    import torch
+    codes = {torch.float32: TI_DTYPE_F32, torch.bfloat16: TI_DTYPE_BF16, torch.float16: TI_DTYPE_F16}
+    rows, k = w.shape
+    packed = torch.empty((rows, k // 2), dtype=torch.uint8, device=w.device)
+    scale = torch.empty((rows, k // 32), dtype=torch.uint8, device=w.device)
+    flags = torch.empty((1,), dtype=torch.int32, device=w.device)
+    st = lib().tinyinfer_mxfp4_quantize(w.data_ptr(), codes[w.dtype], rows, k, packed.data_ptr(),
+                                        scale.data_ptr(), flags.data_ptr(), _stream_handle(stream))
+    _check(st, "tinyinfer_mxfp4_quantize")
+    return packed, scale, flags

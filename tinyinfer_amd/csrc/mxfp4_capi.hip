@@ -1,0 +1,139 @@
+// C ABI of the MXFP4 MLP library (declared in include/tinyinfer_mxfp4.h).
+//
+// Replaces the reference's extern "C" mlp_forward_mxfp4_cuda
+// (tinyinfer/csrc/mlp_fp4.cu:466-518): same arguments plus an explicit
+// stream; validation failures and HIP errors come back as status codes
+// instead of thrown exceptions, so the boundary is safe for any FFI.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstring>
+
+#include "../../include/tinyinfer_mxfp4.h"
+#include "mxfp4_common.hpp"
+#include "mxfp4_launch.hpp"
+
+namespace {
+
+using tinyinfer::MlpArgs;
+
+// Largest index any kernel forms in 64-bit is fine; grid dimensions and the
+// per-row chunk counts are 32-bit, so cap sizes well below that.
+constexpr size_t kMaxDim = size_t(1) << 30;
+constexpr size_t kMaxTokens = size_t(1) << 24;
+
+// Per-device "is gfx950" cache: 0 unknown, 1 yes, 2 no.
+std::atomic<int> g_arch_ok[64];
+
+int check_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return TI_ERR_NO_DEVICE;
+  if (dev < 0 || dev >= 64) return TI_ERR_NO_DEVICE;
+  int st = g_arch_ok[dev].load(std::memory_order_relaxed);
+  if (st == 0) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return TI_ERR_NO_DEVICE;
+    st = (std::strncmp(prop.gcnArchName, "gfx950", 6) == 0) ? 1 : 2;
+    g_arch_ok[dev].store(st, std::memory_order_relaxed);
+  }
+  return st == 1 ? TI_OK : TI_ERR_NO_DEVICE;
+}
+
+int to_status(hipError_t e) { return e == hipSuccess ? TI_OK : TI_ERR_HIP; }
+
+int validate_mlp(const void* X, const uint8_t* gate, const uint8_t* gate_scale, const uint8_t* up,
+                 const uint8_t* up_scale, const uint8_t* down, const uint8_t* down_scale, size_t N,
+                 size_t hidden, size_t inter, void* tmp, void* O, int dtype) {
+  if (!X || !gate || !gate_scale || !up || !up_scale || !down || !down_scale || !tmp || !O)
+    return TI_ERR_INVALID_ARG;
+  if (N == 0 || hidden == 0 || inter == 0) return TI_ERR_INVALID_ARG;
+  if (hidden % 32 != 0 || inter % 32 != 0) return TI_ERR_BAD_SHAPE;
+  if (dtype != TI_DTYPE_F16 && dtype != TI_DTYPE_BF16) return TI_ERR_BAD_DTYPE;
+  if (N > kMaxTokens || hidden > kMaxDim || inter > kMaxDim) return TI_ERR_TOO_LARGE;
+  return TI_OK;
+}
+
+// Token count from which the tiled GEMM beats the skinny path (weights are
+// re-streamed once per 64 tokens on the skinny path).
+constexpr size_t kGemmMinTokens = 96;
+
+int mlp_impl(const void* X, const uint8_t* gate, const uint8_t* gate_scale, const uint8_t* up,
+             const uint8_t* up_scale, const uint8_t* down, const uint8_t* down_scale, size_t N,
+             size_t hidden, size_t inter, void* tmp, void* O, int dtype, int path, void* stream) {
+  int st = validate_mlp(X, gate, gate_scale, up, up_scale, down, down_scale, N, hidden, inter, tmp, O,
+                        dtype);
+  if (st != TI_OK) return st;
+  if (path != TI_PATH_AUTO && path != TI_PATH_SKINNY && path != TI_PATH_GEMM) return TI_ERR_INVALID_ARG;
+  st = check_device();
+  if (st != TI_OK) return st;
+  MlpArgs a{X, gate, gate_scale, up, up_scale, down, down_scale, (int64_t)N, (int64_t)hidden,
+            (int64_t)inter, tmp, O, dtype};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (path == TI_PATH_AUTO) path = (N >= kGemmMinTokens) ? TI_PATH_GEMM : TI_PATH_SKINNY;
+  return to_status(path == TI_PATH_GEMM ? tinyinfer::launch_gemm_mlp(a, s)
+                                        : tinyinfer::launch_skinny_mlp(a, s));
+}
+
+}  // namespace
+
+extern "C" {
+
+int tinyinfer_mlp_forward_mxfp4(const void* X, const uint8_t* gate, const uint8_t* gate_scale,
+                                const uint8_t* up, const uint8_t* up_scale, const uint8_t* down,
+                                const uint8_t* down_scale, size_t N, size_t hidden_dim,
+                                size_t intermediate, void* tmp, void* O, int dtype_code,
+                                void* stream) {
+  return mlp_impl(X, gate, gate_scale, up, up_scale, down, down_scale, N, hidden_dim, intermediate,
+                  tmp, O, dtype_code, TI_PATH_AUTO, stream);
+}
+
+int tinyinfer_mlp_forward_mxfp4_path(const void* X, const uint8_t* gate, const uint8_t* gate_scale,
+                                     const uint8_t* up, const uint8_t* up_scale,
+                                     const uint8_t* down, const uint8_t* down_scale, size_t N,
+                                     size_t hidden_dim, size_t intermediate, void* tmp, void* O,
+                                     int dtype_code, int path, void* stream) {
+  return mlp_impl(X, gate, gate_scale, up, up_scale, down, down_scale, N, hidden_dim, intermediate,
+                  tmp, O, dtype_code, path, stream);
+}
+
+int tinyinfer_mxfp4_dequant(const uint8_t* packed, const uint8_t* scale, size_t rows, size_t k,
+                            void* out, int out_dtype, void* stream) {
+  if (!packed || !scale || !out) return TI_ERR_INVALID_ARG;
+  if (k % 32 != 0) return TI_ERR_BAD_SHAPE;
+  if (out_dtype != TI_DTYPE_F32 && out_dtype != TI_DTYPE_BF16) return TI_ERR_BAD_DTYPE;
+  if (rows > kMaxDim || k > kMaxDim) return TI_ERR_TOO_LARGE;
+  int st = check_device();
+  if (st != TI_OK) return st;
+  return to_status(tinyinfer::launch_dequant(packed, scale, (int64_t)rows, (int64_t)k, out, out_dtype,
+                                             static_cast<hipStream_t>(stream)));
+}
+
+int tinyinfer_mxfp4_quantize(const void* w, int in_dtype, size_t rows, size_t k, uint8_t* packed,
+                             uint8_t* scale, uint32_t* flags, void* stream) {
+  if (!w || !packed || !scale || !flags) return TI_ERR_INVALID_ARG;
+  if (k % 32 != 0) return TI_ERR_BAD_SHAPE;
+  if (in_dtype != TI_DTYPE_F32 && in_dtype != TI_DTYPE_BF16 && in_dtype != TI_DTYPE_F16)
+    return TI_ERR_BAD_DTYPE;
+  if (rows > kMaxDim || k > kMaxDim) return TI_ERR_TOO_LARGE;
+  int st = check_device();
+  if (st != TI_OK) return st;
+  return to_status(tinyinfer::launch_quantize(w, in_dtype, (int64_t)rows, (int64_t)k, packed, scale,
+                                              flags, static_cast<hipStream_t>(stream)));
+}
+
+const char* tinyinfer_mxfp4_status_string(int status) {
+  switch (status) {
+    case TI_OK: return "ok";
+    case TI_ERR_INVALID_ARG: return "invalid argument";
+    case TI_ERR_BAD_SHAPE: return "hidden_dim and intermediate must be divisible by 32";
+    case TI_ERR_BAD_DTYPE: return "unsupported dtype";
+    case TI_ERR_HIP: return "HIP runtime error";
+    case TI_ERR_NO_DEVICE: return "no gfx950 (MI355X) device is current";
+    case TI_ERR_TOO_LARGE: return "size exceeds kernel limits";
+    default: return "unknown status";
+  }
+}
+
+int tinyinfer_mxfp4_abi_version(void) { return 1; }
+
+}  // extern "C"

@@ -1,0 +1,40 @@
+// Internal host-side launchers shared between the kernel translation units and
+// the C ABI (mxfp4_capi.hip). Not part of the public interface.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace tinyinfer {
+
+struct MlpArgs {
+  const void* x;            // [n, hidden] activation dtype
+  const uint8_t* gate;      // [inter, hidden/2]
+  const uint8_t* gate_scale;
+  const uint8_t* up;        // [inter, hidden/2]
+  const uint8_t* up_scale;
+  const uint8_t* down;      // [hidden, inter/2]
+  const uint8_t* down_scale;
+  int64_t n;
+  int64_t hidden;
+  int64_t inter;
+  void* tmp;                // [n, inter] activation dtype
+  void* out;                // [n, hidden] activation dtype
+  int dtype;                // kF16 / kBF16
+};
+
+// Skinny path: weights streamed once per 64 tokens (MFMA 16x16x32, weights as
+// the 16-row operand). Any n >= 1.
+hipError_t launch_skinny_mlp(const MlpArgs& a, hipStream_t stream);
+
+// Tiled MFMA GEMM path (n >= 128 preferred; any n >= 1 is correct).
+hipError_t launch_gemm_mlp(const MlpArgs& a, hipStream_t stream);
+
+hipError_t launch_dequant(const uint8_t* packed, const uint8_t* scale, int64_t rows, int64_t k,
+                          void* out, int out_dtype, hipStream_t stream);
+
+hipError_t launch_quantize(const void* w, int in_dtype, int64_t rows, int64_t k, uint8_t* packed,
+                           uint8_t* scale, uint32_t* flags, hipStream_t stream);
+
+}  // namespace tinyinfer

@@ -1,0 +1,86 @@
+"""Benchmark/test workloads: the MLP shapes of the target configurations,
+their algorithmic byte and flop counts, and seeded synthetic inputs.
+
+Shapes: Qwen3 hidden/intermediate sizes.  Work per MLP call:
+  bytes = 3*H*I/2 (e2m1 nibbles) + 3*H*I/32 (e8m0 scales) + 2*M*H (x) + 2*M*H (out)
+  flops = 6*M*H*I   (three GEMMs; the SiLU*up epilogue is not counted)
+The h round trip (4*M*I bytes) is not counted, since a fused kernel need not
+make it.
+
+Synthetic inputs: weights N(0, 0.02) with seeds 1000 + 3*layer + {0 gate,
+1 up, 2 down}, quantized with the device quantizer; activations N(0, 1) with
+seed 7, cast to the activation dtype.  ``generator="cpu"`` draws with
+torch's CPU generator (tests, small shapes); ``"cuda"`` draws on the GPU
+(benchmark, multi-GB weight sets).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+
+@dataclass(frozen=True)
+class MlpShape:
+    name: str
+    hidden: int
+    inter: int
+    layers: int = 1
+
+
+SHAPES = {
+    "qwen3-0.6b": MlpShape("qwen3-0.6b", 1024, 3072),
+    "qwen3-1.7b": MlpShape("qwen3-1.7b", 2048, 6144),
+    "qwen3-8b": MlpShape("qwen3-8b", 4096, 12288),
+    "qwen3-32b": MlpShape("qwen3-32b", 5120, 25600, 64),
+}
+
+WEIGHT_STD = 0.02
+X_SEED = 7
+
+
+def weight_bytes(h: int, i: int) -> int:
+    return 3 * h * i // 2 + 3 * h * i // 32
+
+
+def alg_bytes(m: int, h: int, i: int) -> int:
+    return weight_bytes(h, i) + 4 * m * h
+
+
+def alg_flops(m: int, h: int, i: int) -> int:
+    return 6 * m * h * i
+
+
+def weight_seeds(layer: int):
+    base = 1000 + 3 * layer
+    return base, base + 1, base + 2
+
+
+def _randn(shape, seed: int, generator: str, device) -> torch.Tensor:
+    g = torch.Generator(device=generator).manual_seed(seed)
+    return torch.randn(shape, generator=g, device=generator, dtype=torch.float32)
+
+
+def random_weights(h: int, i: int, layer: int = 0, generator: str = "cpu"):
+    """fp32 N(0, 0.02) gate [i,h], up [i,h], down [h,i] on ``generator``'s device."""
+    sg, su, sd = weight_seeds(layer)
+    return (_randn((i, h), sg, generator, None) * WEIGHT_STD,
+            _randn((i, h), su, generator, None) * WEIGHT_STD,
+            _randn((h, i), sd, generator, None) * WEIGHT_STD)
+
+
+def quantized_weights(h: int, i: int, layer: int = 0, generator: str = "cuda", device="cuda"):
+    """(gate_packed, gate_scale, up_packed, up_scale, down_packed, down_scale) on
+    ``device``, quantized by the device quantizer."""
+    from .quantization import quantize_chunk
+    out = []
+    for w in random_weights(h, i, layer, generator):
+        p, s = quantize_chunk(w.to(device))
+        out.extend((p, s))
+        del w
+    return tuple(out)
+
+
+def activations(m: int, h: int, dtype=torch.bfloat16, seed: int = X_SEED, generator: str = "cpu", device="cuda"):
+    return _randn((m, h), seed, generator, None).to(dtype).to(device)
