@@ -81,6 +81,28 @@ int tinyinfer_mlp_forward_mxfp4_path(const void* X, const uint8_t* gate, const u
                                      int dtype_code, int path, void* stream);
 
 /*
+ * The gate_up stage alone: tmp = SiLU(X gate^T) * (X up^T), rounded once to
+ * the activation dtype. Replaces the reference's first kernel,
+ * mlp_stage1_mxfp4 (tinyinfer/csrc/mlp_fp4.cu:79-142, launched at :457);
+ * `path` as in tinyinfer_mlp_forward_mxfp4_path. The down pointers of the
+ * full entry point are not taken.
+ */
+int tinyinfer_mlp_gate_up_mxfp4(const void* X, const uint8_t* gate, const uint8_t* gate_scale,
+                                const uint8_t* up, const uint8_t* up_scale, size_t N,
+                                size_t hidden_dim, size_t intermediate, void* tmp, int dtype_code,
+                                int path, void* stream);
+
+/*
+ * The down stage alone: O = tmp down^T, rounded once to the activation dtype.
+ * Replaces the reference's second kernel, mlp_stage2_mxfp4
+ * (tinyinfer/csrc/mlp_fp4.cu:365-426, launched at :459). `tmp` is
+ * [N, intermediate] in the activation dtype.
+ */
+int tinyinfer_mlp_down_mxfp4(const void* tmp, const uint8_t* down, const uint8_t* down_scale,
+                             size_t N, size_t hidden_dim, size_t intermediate, void* O,
+                             int dtype_code, int path, void* stream);
+
+/*
  * Device dequantization: out[rows, k] = e2m1(packed) * 2^(scale-127), bit-exact.
  * Replaces dequantize_chunk (tinyinfer/quantization/quantize_mxfp4.py:67-85)
  * and the device decode helpers decode_e2m1 / decode_e8m0

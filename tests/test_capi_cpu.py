@@ -48,7 +48,7 @@ def test_python_constants_match_header(capi):
 
 
 def test_abi_version_and_status_strings(capi):
-    assert capi.lib().tinyinfer_mxfp4_abi_version() == 1
+    assert capi.lib().tinyinfer_mxfp4_abi_version() == 2
     assert capi.status_string(0) == "ok"
     assert "32" in capi.status_string(capi.TI_ERR_BAD_SHAPE)
     assert capi.status_string(999) == "unknown status"
@@ -70,6 +70,15 @@ def test_validation_before_device_work(capi):
     # forced path out of range
     g = L.tinyinfer_mlp_forward_mxfp4_path
     assert g(p, p, p, p, p, p, p, 1, 64, 64, p, p, 1, 7, None) in (capi.TI_ERR_INVALID_ARG,)
+    # stage entry points: the pointers of the other stage may be null
+    gu = L.tinyinfer_mlp_gate_up_mxfp4
+    assert gu(p, p, p, p, None, 1, 64, 64, p, 1, 0, None) == capi.TI_ERR_INVALID_ARG
+    assert gu(p, p, p, p, p, 1, 64, 40, p, 1, 0, None) == capi.TI_ERR_BAD_SHAPE
+    assert gu(p, p, p, p, p, 1, 64, 64, p, 2, 0, None) == capi.TI_ERR_BAD_DTYPE
+    dn = L.tinyinfer_mlp_down_mxfp4
+    assert dn(p, p, None, 1, 64, 64, p, 1, 0, None) == capi.TI_ERR_INVALID_ARG
+    assert dn(p, p, p, 0, 64, 64, p, 1, 0, None) == capi.TI_ERR_INVALID_ARG
+    assert dn(p, p, p, 1, 64, 64, p, 1, 3, None) == capi.TI_ERR_INVALID_ARG
     assert L.tinyinfer_mxfp4_dequant(p, p, 4, 48, p, 2, None) == capi.TI_ERR_BAD_SHAPE
     assert L.tinyinfer_mxfp4_dequant(p, p, 4, 64, p, 0, None) == capi.TI_ERR_BAD_DTYPE
     assert L.tinyinfer_mxfp4_quantize(p, 2, 4, 64, p, p, None, None) == capi.TI_ERR_INVALID_ARG
@@ -81,6 +90,7 @@ def test_no_device_reports_no_device(capi):
     p = 0x1000
     st = capi.lib().tinyinfer_mlp_forward_mxfp4(p, p, p, p, p, p, p, 1, 64, 64, p, p, 1, None)
     assert st == capi.TI_ERR_NO_DEVICE
+    assert capi.lib().tinyinfer_mlp_down_mxfp4(p, p, p, 1, 64, 64, p, 1, 0, None) == capi.TI_ERR_NO_DEVICE
 
 
 def _cpu_inputs(m=2, h=64, i=96, xdtype=torch.bfloat16):

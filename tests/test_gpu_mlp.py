@@ -212,3 +212,20 @@ def test_nan_scale_propagates_like_reference_gpu(capi):
         mask = torch.ones(64, dtype=torch.bool)
         mask[5] = False
         assert torch.isfinite(out[:, mask]).all()
+
+
+@pytest.mark.parametrize("m", [1, 5, 130])
+def test_stage_entry_points_compose_to_full_call(capi, m):
+    """tinyinfer_mlp_gate_up_mxfp4 followed by tinyinfer_mlp_down_mxfp4 gives
+    bit-identical tmp and output to tinyinfer_mlp_forward_mxfp4 on each path."""
+    banner(f"stages m={m}")
+    x, mats = make_case(m, 256, 384, seed=40 + m)
+    xd, md = to_dev(x, mats)
+    for path in PATHS:
+        tmp_full = torch.empty((m, 384), dtype=xd.dtype, device="cuda")
+        full = capi.mlp_forward(xd, *md, tmp=tmp_full, path=path)
+        tmp = capi.gate_up(xd, *md[:4], path=path)
+        out = capi.down(tmp, *md[4:], path=path)
+        torch.cuda.synchronize()
+        assert torch.equal(tmp.view(torch.int16), tmp_full.view(torch.int16)), path
+        assert torch.equal(out.view(torch.int16), full.view(torch.int16)), path

@@ -38,6 +38,8 @@ _vp, _u8p, _sz, _int = ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes
 SIGNATURES = {
     "tinyinfer_mlp_forward_mxfp4": (_int, [_vp, _u8p, _u8p, _u8p, _u8p, _u8p, _u8p, _sz, _sz, _sz, _vp, _vp, _int, _vp]),
     "tinyinfer_mlp_forward_mxfp4_path": (_int, [_vp, _u8p, _u8p, _u8p, _u8p, _u8p, _u8p, _sz, _sz, _sz, _vp, _vp, _int, _int, _vp]),
+    "tinyinfer_mlp_gate_up_mxfp4": (_int, [_vp, _u8p, _u8p, _u8p, _u8p, _sz, _sz, _sz, _vp, _int, _int, _vp]),
+    "tinyinfer_mlp_down_mxfp4": (_int, [_vp, _u8p, _u8p, _sz, _sz, _sz, _vp, _int, _int, _vp]),
     "tinyinfer_mxfp4_dequant": (_int, [_u8p, _u8p, _sz, _sz, _vp, _int, _vp]),
     "tinyinfer_mxfp4_quantize": (_int, [_vp, _int, _sz, _sz, _u8p, _u8p, _vp, _vp]),
     "tinyinfer_mxfp4_status_string": (ctypes.c_char_p, [_int]),
@@ -103,6 +105,34 @@ def mlp_forward(x, gp, gs, up, us, dp, ds, out=None, tmp=None, path: int = TI_PA
         x.data_ptr(), gp.data_ptr(), gs.data_ptr(), up.data_ptr(), us.data_ptr(), dp.data_ptr(), ds.data_ptr(),
         n, hidden, inter, tmp.data_ptr(), out.data_ptr(), _act_code(x.dtype), int(path), _stream_handle(stream))
     _check(st, "tinyinfer_mlp_forward_mxfp4")
+    return out
+
+
+def gate_up(x, gp, gs, up, us, tmp=None, path: int = TI_PATH_AUTO, stream=None):
+    """The gate_up stage alone: returns tmp = SiLU(x gate^T) * (x up^T) [N, intermediate]."""
+    import torch
+    n, hidden = x.shape
+    inter = gp.shape[0]
+    if tmp is None:
+        tmp = torch.empty((n, inter), dtype=x.dtype, device=x.device)
+    st = lib().tinyinfer_mlp_gate_up_mxfp4(
+        x.data_ptr(), gp.data_ptr(), gs.data_ptr(), up.data_ptr(), us.data_ptr(), n, hidden, inter,
+        tmp.data_ptr(), _act_code(x.dtype), int(path), _stream_handle(stream))
+    _check(st, "tinyinfer_mlp_gate_up_mxfp4")
+    return tmp
+
+
+def down(tmp, dp, ds, out=None, path: int = TI_PATH_AUTO, stream=None):
+    """The down stage alone: returns out = tmp down^T [N, hidden]."""
+    import torch
+    n, inter = tmp.shape
+    hidden = dp.shape[0]
+    if out is None:
+        out = torch.empty((n, hidden), dtype=tmp.dtype, device=tmp.device)
+    st = lib().tinyinfer_mlp_down_mxfp4(
+        tmp.data_ptr(), dp.data_ptr(), ds.data_ptr(), n, hidden, inter, out.data_ptr(),
+        _act_code(tmp.dtype), int(path), _stream_handle(stream))
+    _check(st, "tinyinfer_mlp_down_mxfp4")
     return out
 
 

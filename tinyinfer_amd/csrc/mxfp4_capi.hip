@@ -41,15 +41,18 @@ int check_device() {
 
 int to_status(hipError_t e) { return e == hipSuccess ? TI_OK : TI_ERR_HIP; }
 
-int validate_mlp(const void* X, const uint8_t* gate, const uint8_t* gate_scale, const uint8_t* up,
-                 const uint8_t* up_scale, const uint8_t* down, const uint8_t* down_scale, size_t N,
-                 size_t hidden, size_t inter, void* tmp, void* O, int dtype) {
-  if (!X || !gate || !gate_scale || !up || !up_scale || !down || !down_scale || !tmp || !O)
+// Checks shared by every MLP entry point; `stage` says which pointers the
+// call reads and writes (the others may be null).
+int validate_mlp(const MlpArgs& a, int stage) {
+  if (!a.tmp) return TI_ERR_INVALID_ARG;
+  if ((stage & tinyinfer::kStageGateUp) && (!a.x || !a.gate || !a.gate_scale || !a.up || !a.up_scale))
     return TI_ERR_INVALID_ARG;
-  if (N == 0 || hidden == 0 || inter == 0) return TI_ERR_INVALID_ARG;
-  if (hidden % 32 != 0 || inter % 32 != 0) return TI_ERR_BAD_SHAPE;
-  if (dtype != TI_DTYPE_F16 && dtype != TI_DTYPE_BF16) return TI_ERR_BAD_DTYPE;
-  if (N > kMaxTokens || hidden > kMaxDim || inter > kMaxDim) return TI_ERR_TOO_LARGE;
+  if ((stage & tinyinfer::kStageDown) && (!a.down || !a.down_scale || !a.out)) return TI_ERR_INVALID_ARG;
+  if (a.n <= 0 || a.hidden <= 0 || a.inter <= 0) return TI_ERR_INVALID_ARG;
+  if (a.hidden % 32 != 0 || a.inter % 32 != 0) return TI_ERR_BAD_SHAPE;
+  if (a.dtype != TI_DTYPE_F16 && a.dtype != TI_DTYPE_BF16) return TI_ERR_BAD_DTYPE;
+  if ((size_t)a.n > kMaxTokens || (size_t)a.hidden > kMaxDim || (size_t)a.inter > kMaxDim)
+    return TI_ERR_TOO_LARGE;
   return TI_OK;
 }
 
@@ -57,22 +60,20 @@ int validate_mlp(const void* X, const uint8_t* gate, const uint8_t* gate_scale, 
 // re-streamed once per 64 tokens on the skinny path).
 constexpr size_t kGemmMinTokens = 96;
 
-int mlp_impl(const void* X, const uint8_t* gate, const uint8_t* gate_scale, const uint8_t* up,
-             const uint8_t* up_scale, const uint8_t* down, const uint8_t* down_scale, size_t N,
-             size_t hidden, size_t inter, void* tmp, void* O, int dtype, int path, void* stream) {
-  int st = validate_mlp(X, gate, gate_scale, up, up_scale, down, down_scale, N, hidden, inter, tmp, O,
-                        dtype);
+int mlp_impl(const MlpArgs& a, int stage, int path, void* stream) {
+  // sizes arrive as size_t; anything that wraps negative is rejected here
+  int st = validate_mlp(a, stage);
   if (st != TI_OK) return st;
   if (path != TI_PATH_AUTO && path != TI_PATH_SKINNY && path != TI_PATH_GEMM) return TI_ERR_INVALID_ARG;
   st = check_device();
   if (st != TI_OK) return st;
-  MlpArgs a{X, gate, gate_scale, up, up_scale, down, down_scale, (int64_t)N, (int64_t)hidden,
-            (int64_t)inter, tmp, O, dtype};
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (path == TI_PATH_AUTO) path = (N >= kGemmMinTokens) ? TI_PATH_GEMM : TI_PATH_SKINNY;
-  return to_status(path == TI_PATH_GEMM ? tinyinfer::launch_gemm_mlp(a, s)
-                                        : tinyinfer::launch_skinny_mlp(a, s));
+  if (path == TI_PATH_AUTO) path = ((size_t)a.n >= kGemmMinTokens) ? TI_PATH_GEMM : TI_PATH_SKINNY;
+  return to_status(path == TI_PATH_GEMM ? tinyinfer::launch_gemm_mlp(a, stage, s)
+                                        : tinyinfer::launch_skinny_mlp(a, stage, s));
 }
+
+int64_t as_dim(size_t v) { return v > (size_t)INT64_MAX ? -1 : (int64_t)v; }
 
 }  // namespace
 
@@ -83,8 +84,9 @@ int tinyinfer_mlp_forward_mxfp4(const void* X, const uint8_t* gate, const uint8_
                                 const uint8_t* down_scale, size_t N, size_t hidden_dim,
                                 size_t intermediate, void* tmp, void* O, int dtype_code,
                                 void* stream) {
-  return mlp_impl(X, gate, gate_scale, up, up_scale, down, down_scale, N, hidden_dim, intermediate,
-                  tmp, O, dtype_code, TI_PATH_AUTO, stream);
+  MlpArgs a{X, gate, gate_scale, up, up_scale, down, down_scale, as_dim(N), as_dim(hidden_dim),
+            as_dim(intermediate), tmp, O, dtype_code};
+  return mlp_impl(a, tinyinfer::kStageBoth, TI_PATH_AUTO, stream);
 }
 
 int tinyinfer_mlp_forward_mxfp4_path(const void* X, const uint8_t* gate, const uint8_t* gate_scale,
@@ -92,8 +94,26 @@ int tinyinfer_mlp_forward_mxfp4_path(const void* X, const uint8_t* gate, const u
                                      const uint8_t* down, const uint8_t* down_scale, size_t N,
                                      size_t hidden_dim, size_t intermediate, void* tmp, void* O,
                                      int dtype_code, int path, void* stream) {
-  return mlp_impl(X, gate, gate_scale, up, up_scale, down, down_scale, N, hidden_dim, intermediate,
-                  tmp, O, dtype_code, path, stream);
+  MlpArgs a{X, gate, gate_scale, up, up_scale, down, down_scale, as_dim(N), as_dim(hidden_dim),
+            as_dim(intermediate), tmp, O, dtype_code};
+  return mlp_impl(a, tinyinfer::kStageBoth, path, stream);
+}
+
+int tinyinfer_mlp_gate_up_mxfp4(const void* X, const uint8_t* gate, const uint8_t* gate_scale,
+                                const uint8_t* up, const uint8_t* up_scale, size_t N,
+                                size_t hidden_dim, size_t intermediate, void* tmp, int dtype_code,
+                                int path, void* stream) {
+  MlpArgs a{X, gate, gate_scale, up, up_scale, nullptr, nullptr, as_dim(N), as_dim(hidden_dim),
+            as_dim(intermediate), tmp, nullptr, dtype_code};
+  return mlp_impl(a, tinyinfer::kStageGateUp, path, stream);
+}
+
+int tinyinfer_mlp_down_mxfp4(const void* tmp, const uint8_t* down, const uint8_t* down_scale,
+                             size_t N, size_t hidden_dim, size_t intermediate, void* O,
+                             int dtype_code, int path, void* stream) {
+  MlpArgs a{nullptr, nullptr, nullptr, nullptr, nullptr, down, down_scale, as_dim(N),
+            as_dim(hidden_dim), as_dim(intermediate), const_cast<void*>(tmp), O, dtype_code};
+  return mlp_impl(a, tinyinfer::kStageDown, path, stream);
 }
 
 int tinyinfer_mxfp4_dequant(const uint8_t* packed, const uint8_t* scale, size_t rows, size_t k,
@@ -134,6 +154,6 @@ const char* tinyinfer_mxfp4_status_string(int status) {
   }
 }
 
-int tinyinfer_mxfp4_abi_version(void) { return 1; }
+int tinyinfer_mxfp4_abi_version(void) { return 2; }
 
 }  // extern "C"

@@ -24,12 +24,16 @@ struct MlpArgs {
   int dtype;                // kF16 / kBF16
 };
 
+// Which part of the MLP a launcher runs: the gate_up stage (tmp = SiLU(x G^T) *
+// (x U^T)), the down stage (out = tmp D^T), or both in order.
+enum Stage : int { kStageGateUp = 1, kStageDown = 2, kStageBoth = 3 };
+
 // Skinny path: weights streamed once per 64 tokens (MFMA 16x16x32, weights as
 // the 16-row operand). Any n >= 1.
-hipError_t launch_skinny_mlp(const MlpArgs& a, hipStream_t stream);
+hipError_t launch_skinny_mlp(const MlpArgs& a, int stage, hipStream_t stream);
 
 // Tiled MFMA GEMM path (n >= 128 preferred; any n >= 1 is correct).
-hipError_t launch_gemm_mlp(const MlpArgs& a, hipStream_t stream);
+hipError_t launch_gemm_mlp(const MlpArgs& a, int stage, hipStream_t stream);
 
 hipError_t launch_dequant(const uint8_t* packed, const uint8_t* scale, int64_t rows, int64_t k,
                           void* out, int out_dtype, hipStream_t stream);

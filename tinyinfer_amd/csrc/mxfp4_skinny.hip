@@ -18,6 +18,13 @@
 //   * Waves of a workgroup split K (and, for gate_up, the two matrices); an
 //     LDS reduction combines them and the epilogue applies SiLU(g)*u (gate_up)
 //     or plain rounding (down).
+//
+// Memory pipeline: a wave owns at most NCH chunks and issues every weight and
+// scale load of them before its first MFMA, so the whole grid puts (nearly)
+// the whole weight matrix in flight at once and pays the HBM latency once;
+// activations are fetched one chunk ahead of the MFMAs that use them.
+#include <cstdlib>
+
 #include "mxfp4_common.hpp"
 #include "mxfp4_launch.hpp"
 
@@ -27,80 +34,118 @@ namespace {
 
 constexpr int kChunkK = 128;      // K elements per lane-group load (64 lanes x 16 B)
 
-// Chunks in flight per wave: 4 at one token tile, fewer as the per-chunk
-// activation registers (T tiles x 4 dwordx4) grow.
 template <int T>
-constexpr int unroll_for() { return T == 1 ? 4 : (T == 2 ? 2 : 1); }
-
-template <int DT>
-__device__ __forceinline__ u32x4_t load_act8(const uint16_t* p, bool ok) {
-  u32x4_t v = {0u, 0u, 0u, 0u};
-  if (ok) v = *reinterpret_cast<const u32x4_t*>(p);
-  return v;
+__device__ __forceinline__ void load_x_chunk(const uint16_t* __restrict__ x, int64_t m_base, int64_t M,
+                                             int64_t K, int64_t k0, bool ok, int r, u32x4_t (&dst)[T * 4]) {
+#pragma unroll
+  for (int tt = 0; tt < T; ++tt) {
+    const int64_t tok = m_base + tt * 16 + r;
+    const bool tok_ok = ok && tok < M;
+    const uint16_t* xp = x + (tok_ok ? tok : 0) * K + (ok ? k0 : 0);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      u32x4_t v = {0u, 0u, 0u, 0u};
+      if (tok_ok) v = *reinterpret_cast<const u32x4_t*>(xp + 8 * t);
+      dst[tt * 4 + t] = v;
+    }
+  }
 }
 
-// One wave's contribution: rows [row0, row0+16) of W, K chunks [c0, c1).
-template <int DT, int T>
-__device__ __forceinline__ void wave_skinny(const uint16_t* __restrict__ x, const uint8_t* __restrict__ w,
+// One batch of a wave's work: rows [row0, row0+16) of W, K chunks [c0, c1),
+// c1 - c0 <= NCH.
+template <int DT, int T, int NCH>
+__device__ __forceinline__ void wave_batch(const uint16_t* __restrict__ x, const uint8_t* __restrict__ w,
                                             const uint8_t* __restrict__ ws, int64_t m_base, int64_t M,
                                             int64_t K, int64_t R, int64_t row0, int c0, int c1,
                                             f32x4_t (&acc)[T]) {
   const int lane = threadIdx.x & 63;
   const int r = lane & 15;
   const int q = lane >> 4;
-  const int64_t row = row0 + r;
-  const bool row_ok = row < R;
-  const int64_t rowc = row_ok ? row : 0;
-  const uint8_t* wrow = w + rowc * (K / 2);
-  const uint8_t* srow = ws + rowc * (K / 32);
-  constexpr int kUnroll = unroll_for<T>();
-  for (int c = c0; c < c1; c += kUnroll) {
-    u32x4_t wv[kUnroll];
-    uint32_t sb[kUnroll];
-    u32x4_t xv[kUnroll][T][4];
+  // R is a multiple of 32 (checked at the C ABI), so every row of the tile exists.
+  const uint8_t* wrow = w + (row0 + r) * (K / 2) + 16 * q;
+  const uint8_t* srow = ws + (row0 + r) * (K / 32) + q;
+
+  // 1. every weight and scale load of this wave, back to back
+  u32x4_t wv[NCH];
+  uint32_t sb[NCH];
+  if (c1 - c0 == NCH && (int64_t)c1 * kChunkK <= K) {
+    // whole batch in bounds: unpredicated loads at immediate offsets
+    const uint8_t* wp = wrow + (int64_t)c0 * (kChunkK / 2);
+    const uint8_t* sp = srow + (int64_t)c0 * (kChunkK / 32);
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t k0 = (int64_t)(c + u) * kChunkK + 32 * q;
-      const bool ok = (c + u < c1) && (k0 < K);
+    for (int u = 0; u < NCH; ++u)
+      wv[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wp + u * (kChunkK / 2)));
+#pragma unroll
+    for (int u = 0; u < NCH; ++u) sb[u] = sp[u * (kChunkK / 32)];
+  } else {
+#pragma unroll
+    for (int u = 0; u < NCH; ++u) {
+      const int64_t k0 = (int64_t)(c0 + u) * kChunkK + 32 * q;
+      const bool ok = (c0 + u < c1) && (k0 < K);
       wv[u] = u32x4_t{0u, 0u, 0u, 0u};
       sb[u] = 127u;
-      if (ok && row_ok) {
-        wv[u] = *reinterpret_cast<const u32x4_t*>(wrow + k0 / 2);
-        sb[u] = srow[k0 / 32];
-      }
-#pragma unroll
-      for (int tt = 0; tt < T; ++tt) {
-        const int64_t tok = m_base + tt * 16 + r;
-        const bool tok_ok = ok && tok < M;
-        const uint16_t* xp = x + (tok_ok ? tok : 0) * K + (ok ? k0 : 0);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) xv[u][tt][t] = load_act8<DT>(xp + 8 * t, tok_ok);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const u32x4_t a = dq8_bf16(wv[u][t], sb[u]);
-#pragma unroll
-        for (int tt = 0; tt < T; ++tt) {
-          if constexpr (DT == kBF16) {
-            acc[tt] = mfma16x16x32(a, xv[u][tt][t], acc[tt]);
-          } else {
-            u32x4_t hi, lo;
-            f16x8_split_bf16(xv[u][tt][t], hi, lo);
-            acc[tt] = mfma16x16x32(a, hi, acc[tt]);
-            acc[tt] = mfma16x16x32(a, lo, acc[tt]);
-          }
-        }
+      if (ok) {
+        wv[u] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4_t*>(wrow + (int64_t)(c0 + u) * (kChunkK / 2)));
+        sb[u] = srow[(int64_t)(c0 + u) * (kChunkK / 32)];
       }
     }
   }
+
+  // 2. activations one chunk ahead, then dequant + MFMA
+  auto chunk_ok = [&](int u, int64_t& k0) {
+    k0 = (int64_t)(c0 + u) * kChunkK + 32 * q;
+    return (c0 + u < c1) && (k0 < K);
+  };
+  auto compute = [&](int u, const u32x4_t (&xc)[T * 4]) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const u32x4_t a = dq8_bf16(wv[u][t], sb[u]);
+#pragma unroll
+      for (int tt = 0; tt < T; ++tt) {
+        if constexpr (DT == kBF16) {
+          acc[tt] = mfma16x16x32(a, xc[tt * 4 + t], acc[tt]);
+        } else {
+          u32x4_t hi, lo;
+          f16x8_split_bf16(xc[tt * 4 + t], hi, lo);
+          acc[tt] = mfma16x16x32(a, hi, acc[tt]);
+          acc[tt] = mfma16x16x32(a, lo, acc[tt]);
+        }
+      }
+    }
+  };
+  u32x4_t xa[T * 4], xb[T * 4];
+  int64_t kx;
+  bool okx = chunk_ok(0, kx);
+  load_x_chunk<T>(x, m_base, M, K, kx, okx, r, xa);
+#pragma unroll
+  for (int u = 0; u < NCH; u += 2) {
+    if (u + 1 < NCH) {
+      okx = chunk_ok(u + 1, kx);
+      load_x_chunk<T>(x, m_base, M, K, kx, okx, r, xb);
+    }
+    if (c0 + u < c1) compute(u, xa);
+    if (u + 2 < NCH) {
+      okx = chunk_ok(u + 2, kx);
+      load_x_chunk<T>(x, m_base, M, K, kx, okx, r, xa);
+    }
+    if (u + 1 < NCH && c0 + u + 1 < c1) compute(u + 1, xb);
+  }
+}
+
+// A wave's whole K slice [c0, c1), in batches of NCH chunks.
+template <int DT, int T, int NCH>
+__device__ __forceinline__ void wave_skinny(const uint16_t* __restrict__ x, const uint8_t* __restrict__ w,
+                                            const uint8_t* __restrict__ ws, int64_t m_base, int64_t M,
+                                            int64_t K, int64_t R, int64_t row0, int c0, int c1,
+                                            f32x4_t (&acc)[T]) {
+  for (int cb = c0; cb < c1; cb += NCH)
+    wave_batch<DT, T, NCH>(x, w, ws, m_base, M, K, R, row0, cb, cb + NCH < c1 ? cb + NCH : c1, acc);
 }
 
 // GATEUP: out = h[M, R] = SiLU(x W0^T) * (x W1^T), K = hidden, R = inter.
 // else:   out = y[M, R] = x W0^T, K = inter, R = hidden.
-template <int DT, int T, bool GATEUP, int NW>
+template <int DT, int T, int NCH, bool GATEUP, int NW>
 __global__ __launch_bounds__(NW * 64) void skinny_kernel(const uint16_t* __restrict__ x,
                                                          const uint8_t* __restrict__ w0,
                                                          const uint8_t* __restrict__ s0,
@@ -123,7 +168,7 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(const uint16_t* __restr
   f32x4_t acc[T];
 #pragma unroll
   for (int tt = 0; tt < T; ++tt) acc[tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  wave_skinny<DT, T>(x, mat ? w1 : w0, mat ? s1 : s0, m_base, M, K, R, row0, c0, c1, acc);
+  wave_skinny<DT, T, NCH>(x, mat ? w1 : w0, mat ? s1 : s0, m_base, M, K, R, row0, c0, c1, acc);
 
 #pragma unroll
   for (int tt = 0; tt < T; ++tt) red[wave][tt][lane] = acc[tt];
@@ -157,57 +202,80 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(const uint16_t* __restr
   }
 }
 
-template <int DT, int T, bool GATEUP, int NW>
+template <int DT, int T, int NCH, bool GATEUP, int NW>
 void launch_one(const uint16_t* x, const uint8_t* w0, const uint8_t* s0, const uint8_t* w1,
                 const uint8_t* s1, int64_t M, int64_t K, int64_t R, uint16_t* out, hipStream_t st) {
   dim3 grid((unsigned)((R + 15) / 16), (unsigned)((M + 16 * T - 1) / (16 * T)));
-  skinny_kernel<DT, T, GATEUP, NW><<<grid, NW * 64, 0, st>>>(x, w0, s0, w1, s1, M, K, R, out);
+  skinny_kernel<DT, T, NCH, GATEUP, NW><<<grid, NW * 64, 0, st>>>(x, w0, s0, w1, s1, M, K, R, out);
 }
 
-// Waves per workgroup: enough K slices that the grid holds >= ~8 waves per CU.
-template <int DT, int T, bool GATEUP>
+// Test/tuning override: TINYINFER_SKINNY_NW=<4|8> forces the waves per
+// workgroup (read once per process).
+int forced_nw() {
+  static const int v = [] {
+    const char* e = std::getenv("TINYINFER_SKINNY_NW");
+    const int n = e ? std::atoi(e) : 0;
+    return (n == 4 || n == 8) ? n : 0;
+  }();
+  return v;
+}
+
+// Waves per workgroup (4 or 8; 16 would cap registers at 128 and spill).
+// 4 when each wave's K slice fits one NCH batch and the grid still has
+// >= 2048 waves (8 per CU); otherwise 8, which halves each slice and doubles
+// the waves.  At the Qwen3-8B shapes this puts the whole matrix in flight in
+// one round of waves: gate_up 768 tiles x 4 waves x 16 chunks, down 256
+// tiles x 8 waves x 12 chunks.
+template <int DT, int T, int NCH, bool GATEUP>
 void launch_nw(const uint16_t* x, const uint8_t* w0, const uint8_t* s0, const uint8_t* w1,
                const uint8_t* s1, int64_t M, int64_t K, int64_t R, uint16_t* out, hipStream_t st) {
   const int64_t tiles = (R + 15) / 16;
   const int64_t chunks = (K + kChunkK - 1) / kChunkK;
-  // target waves in the grid ~ 3072 (256 CUs x 12)
-  int64_t nw = (3072 + tiles - 1) / tiles;
-  if (GATEUP) nw = (nw + 1) & ~int64_t(1);
-  const int64_t max_nw_by_k = GATEUP ? 2 * chunks : chunks;
-  if (nw > max_nw_by_k) nw = max_nw_by_k;
-  if (nw <= 4) launch_one<DT, T, GATEUP, 4>(x, w0, s0, w1, s1, M, K, R, out, st);
-  else if (nw <= 8) launch_one<DT, T, GATEUP, 8>(x, w0, s0, w1, s1, M, K, R, out, st);
-  else launch_one<DT, T, GATEUP, 16>(x, w0, s0, w1, s1, M, K, R, out, st);
+  const int64_t mats = GATEUP ? 2 : 1;
+  int nw = forced_nw();
+  if (nw == 0) {
+    const int64_t per_wave4 = (chunks * mats + 3) / 4;
+    nw = (per_wave4 <= NCH && tiles * 4 >= 2048) ? 4 : 8;
+  }
+  if (nw == 4) launch_one<DT, T, NCH, GATEUP, 4>(x, w0, s0, w1, s1, M, K, R, out, st);
+  else launch_one<DT, T, NCH, GATEUP, 8>(x, w0, s0, w1, s1, M, K, R, out, st);
 }
 
+// Chunk depth per wave: NCH weight dwordx4 loads in flight per lane; fewer
+// as the per-chunk activation registers (T tiles x 2 x 4 dwordx4) grow.
 template <int DT, bool GATEUP>
 void launch_t(const uint16_t* x, const uint8_t* w0, const uint8_t* s0, const uint8_t* w1,
               const uint8_t* s1, int64_t M, int64_t K, int64_t R, uint16_t* out, hipStream_t st) {
   const int64_t t = M >= 64 ? 4 : (M + 15) / 16;
   switch (t) {
-    case 1: launch_nw<DT, 1, GATEUP>(x, w0, s0, w1, s1, M, K, R, out, st); break;
-    case 2: launch_nw<DT, 2, GATEUP>(x, w0, s0, w1, s1, M, K, R, out, st); break;
-    case 3: launch_nw<DT, 3, GATEUP>(x, w0, s0, w1, s1, M, K, R, out, st); break;
-    default: launch_nw<DT, 4, GATEUP>(x, w0, s0, w1, s1, M, K, R, out, st); break;
+    case 1: launch_nw<DT, 1, 16, GATEUP>(x, w0, s0, w1, s1, M, K, R, out, st); break;
+    case 2: launch_nw<DT, 2, 8, GATEUP>(x, w0, s0, w1, s1, M, K, R, out, st); break;
+    case 3: launch_nw<DT, 3, 4, GATEUP>(x, w0, s0, w1, s1, M, K, R, out, st); break;
+    default: launch_nw<DT, 4, 4, GATEUP>(x, w0, s0, w1, s1, M, K, R, out, st); break;
   }
 }
 
 template <int DT>
-hipError_t run(const MlpArgs& a, hipStream_t st) {
+hipError_t run(const MlpArgs& a, int stage, hipStream_t st) {
   const uint16_t* x = static_cast<const uint16_t*>(a.x);
   uint16_t* h = static_cast<uint16_t*>(a.tmp);
   uint16_t* y = static_cast<uint16_t*>(a.out);
-  launch_t<DT, true>(x, a.gate, a.gate_scale, a.up, a.up_scale, a.n, a.hidden, a.inter, h, st);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  launch_t<DT, false>(h, a.down, a.down_scale, nullptr, nullptr, a.n, a.inter, a.hidden, y, st);
-  return hipGetLastError();
+  if (stage & kStageGateUp) {
+    launch_t<DT, true>(x, a.gate, a.gate_scale, a.up, a.up_scale, a.n, a.hidden, a.inter, h, st);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  if (stage & kStageDown) {
+    launch_t<DT, false>(h, a.down, a.down_scale, nullptr, nullptr, a.n, a.inter, a.hidden, y, st);
+    return hipGetLastError();
+  }
+  return hipSuccess;
 }
 
 }  // namespace
 
-hipError_t launch_skinny_mlp(const MlpArgs& a, hipStream_t stream) {
-  return a.dtype == kBF16 ? run<kBF16>(a, stream) : run<kF16>(a, stream);
+hipError_t launch_skinny_mlp(const MlpArgs& a, int stage, hipStream_t stream) {
+  return a.dtype == kBF16 ? run<kBF16>(a, stage, stream) : run<kF16>(a, stage, stream);
 }
 
 }  // namespace tinyinfer

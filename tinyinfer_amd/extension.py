@@ -10,6 +10,7 @@ from functools import lru_cache
 
 @lru_cache(maxsize=1)
 def load_extension():
+    import torch  # noqa: F401  (loads libc10_hip / libtorch that _C links against)
     try:
         from tinyinfer_amd import _C
     except ImportError as exc:
