@@ -48,7 +48,7 @@ def test_python_constants_match_header(capi):
 
 
 def test_abi_version_and_status_strings(capi):
-    assert capi.lib().tinyinfer_mxfp4_abi_version() == 2
+    assert capi.lib().tinyinfer_mxfp4_abi_version() == 3
     assert capi.status_string(0) == "ok"
     assert "32" in capi.status_string(capi.TI_ERR_BAD_SHAPE)
     assert capi.status_string(999) == "unknown status"
@@ -78,7 +78,7 @@ def test_validation_before_device_work(capi):
     dn = L.tinyinfer_mlp_down_mxfp4
     assert dn(p, p, None, 1, 64, 64, p, 1, 0, None) == capi.TI_ERR_INVALID_ARG
     assert dn(p, p, p, 0, 64, 64, p, 1, 0, None) == capi.TI_ERR_INVALID_ARG
-    assert dn(p, p, p, 1, 64, 64, p, 1, 3, None) == capi.TI_ERR_INVALID_ARG
+    assert dn(p, p, p, 1, 64, 64, p, 1, 4, None) == capi.TI_ERR_INVALID_ARG
     assert L.tinyinfer_mxfp4_dequant(p, p, 4, 48, p, 2, None) == capi.TI_ERR_BAD_SHAPE
     assert L.tinyinfer_mxfp4_dequant(p, p, 4, 64, p, 0, None) == capi.TI_ERR_BAD_DTYPE
     assert L.tinyinfer_mxfp4_quantize(p, 2, 4, 64, p, p, None, None) == capi.TI_ERR_INVALID_ARG

@@ -26,12 +26,19 @@ def capi():
 
 
 PATHS = [0, 1, 2]  # auto, skinny, gemm
+DECODE = 3         # fused single-launch decode kernel (N <= 8, hidden/intermediate % 256 == 0)
 
 
 def run_all_paths(capi, x, mats):
+    """Every kernel path that accepts this call; the fused decode path is
+    included where it applies and must refuse (not misbehave) elsewhere."""
     outs = {}
-    for path in PATHS:
-        out = capi.mlp_forward(x, *mats, path=path)
+    for path in PATHS + [DECODE]:
+        try:
+            out = capi.mlp_forward(x, *mats, path=path)
+        except capi.TinyInferError as e:
+            assert path == DECODE and e.status == capi.TI_ERR_UNSUPPORTED, (path, e)
+            continue
         torch.cuda.synchronize()
         outs[path] = out.cpu()
     return outs
@@ -137,20 +144,21 @@ def test_qwen3_8b_against_torch_fp32_reference(capi, m):
     mats = quantized_weights(4096, 12288, layer=0)
     x = activations(m, 4096)
     ref = torch_fp32_reference(x, *mats)
-    for path in PATHS:
+    for path in PATHS + ([DECODE] if m <= 4 else []):
         out = capi.mlp_forward(x, *mats, path=path)
         assert_parity(out, ref, f"8B m={m} path={path}")
     del mats
 
 
-def test_deterministic(capi):
-    banner("determinism")
-    x, mats = make_case(33, 512, 1024, seed=77)
+@pytest.mark.parametrize("m", [3, 33])
+def test_deterministic(capi, m):
+    banner(f"determinism m={m}")
+    x, mats = make_case(m, 512, 1024, seed=77)
     xd, md = to_dev(x, mats)
-    for path in PATHS:
+    for path in PATHS + ([DECODE] if m <= 8 else []):
         a = capi.mlp_forward(xd, *md, path=path)
         b = capi.mlp_forward(xd, *md, path=path)
-        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), path
 
 
 def test_torch_wrapper_and_module_match_capi(capi):
@@ -217,11 +225,12 @@ def test_nan_scale_propagates_like_reference_gpu(capi):
 @pytest.mark.parametrize("m", [1, 5, 130])
 def test_stage_entry_points_compose_to_full_call(capi, m):
     """tinyinfer_mlp_gate_up_mxfp4 followed by tinyinfer_mlp_down_mxfp4 gives
-    bit-identical tmp and output to tinyinfer_mlp_forward_mxfp4 on each path."""
+    bit-identical tmp and output to tinyinfer_mlp_forward_mxfp4 on the same
+    explicit path (the stage entry points have no fused form)."""
     banner(f"stages m={m}")
     x, mats = make_case(m, 256, 384, seed=40 + m)
     xd, md = to_dev(x, mats)
-    for path in PATHS:
+    for path in (1, 2):
         tmp_full = torch.empty((m, 384), dtype=xd.dtype, device="cuda")
         full = capi.mlp_forward(xd, *md, tmp=tmp_full, path=path)
         tmp = capi.gate_up(xd, *md[:4], path=path)

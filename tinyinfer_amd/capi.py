@@ -21,6 +21,8 @@ TI_ERR_BAD_DTYPE = 3
 TI_ERR_HIP = 4
 TI_ERR_NO_DEVICE = 5
 TI_ERR_TOO_LARGE = 6
+TI_ERR_MISALIGNED = 7
+TI_ERR_UNSUPPORTED = 8
 
 TI_DTYPE_F16 = 0
 TI_DTYPE_BF16 = 1
@@ -29,6 +31,7 @@ TI_DTYPE_F32 = 2
 TI_PATH_AUTO = 0
 TI_PATH_SKINNY = 1
 TI_PATH_GEMM = 2
+TI_PATH_DECODE = 3
 
 TI_QFLAG_NONFINITE = 1
 TI_QFLAG_EXP_RANGE = 2
@@ -42,6 +45,7 @@ SIGNATURES = {
     "tinyinfer_mlp_down_mxfp4": (_int, [_vp, _u8p, _u8p, _sz, _sz, _sz, _vp, _int, _int, _vp]),
     "tinyinfer_mxfp4_dequant": (_int, [_u8p, _u8p, _sz, _sz, _vp, _int, _vp]),
     "tinyinfer_mxfp4_quantize": (_int, [_vp, _int, _sz, _sz, _u8p, _u8p, _vp, _vp]),
+    "tinyinfer_mxfp4_diagnostics": (_int, [ctypes.c_void_p]),
     "tinyinfer_mxfp4_status_string": (ctypes.c_char_p, [_int]),
     "tinyinfer_mxfp4_abi_version": (_int, []),
 }
@@ -134,6 +138,13 @@ def down(tmp, dp, ds, out=None, path: int = TI_PATH_AUTO, stream=None):
         _act_code(tmp.dtype), int(path), _stream_handle(stream))
     _check(st, "tinyinfer_mlp_down_mxfp4")
     return out
+
+
+def decode_barrier_timeouts() -> int:
+    """Grid-barrier timeouts of the fused decode kernel on the current device."""
+    v = ctypes.c_uint32(0)
+    _check(lib().tinyinfer_mxfp4_diagnostics(ctypes.byref(v)), "tinyinfer_mxfp4_diagnostics")
+    return int(v.value)
 
 
 def dequant(packed, scale, out_dtype=None, stream=None):

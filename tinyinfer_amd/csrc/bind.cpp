@@ -160,4 +160,5 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.attr("PATH_AUTO") = TI_PATH_AUTO;
   m.attr("PATH_SKINNY") = TI_PATH_SKINNY;
   m.attr("PATH_GEMM") = TI_PATH_GEMM;
+  m.attr("PATH_DECODE") = TI_PATH_DECODE;
 }

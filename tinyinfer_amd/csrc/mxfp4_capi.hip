@@ -43,6 +43,8 @@ int to_status(hipError_t e) { return e == hipSuccess ? TI_OK : TI_ERR_HIP; }
 
 // Checks shared by every MLP entry point; `stage` says which pointers the
 // call reads and writes (the others may be null).
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 int validate_mlp(const MlpArgs& a, int stage) {
   if (!a.tmp) return TI_ERR_INVALID_ARG;
   if ((stage & tinyinfer::kStageGateUp) && (!a.x || !a.gate || !a.gate_scale || !a.up || !a.up_scale))
@@ -53,24 +55,42 @@ int validate_mlp(const MlpArgs& a, int stage) {
   if (a.dtype != TI_DTYPE_F16 && a.dtype != TI_DTYPE_BF16) return TI_ERR_BAD_DTYPE;
   if ((size_t)a.n > kMaxTokens || (size_t)a.hidden > kMaxDim || (size_t)a.inter > kMaxDim)
     return TI_ERR_TOO_LARGE;
+  // 16-byte vector loads of activations and packed weights
+  if (!aligned16(a.tmp)) return TI_ERR_MISALIGNED;
+  if ((stage & tinyinfer::kStageGateUp) && (!aligned16(a.x) || !aligned16(a.gate) || !aligned16(a.up)))
+    return TI_ERR_MISALIGNED;
+  if ((stage & tinyinfer::kStageDown) && !aligned16(a.down)) return TI_ERR_MISALIGNED;
   return TI_OK;
 }
 
 // Token count from which the tiled GEMM beats the skinny path (weights are
 // re-streamed once per 64 tokens on the skinny path).
 constexpr size_t kGemmMinTokens = 96;
+// Token count up to which the streaming decode kernels are used.
+constexpr size_t kStreamMaxTokens = 8;
 
 int mlp_impl(const MlpArgs& a, int stage, int path, void* stream) {
   // sizes arrive as size_t; anything that wraps negative is rejected here
   int st = validate_mlp(a, stage);
   if (st != TI_OK) return st;
-  if (path != TI_PATH_AUTO && path != TI_PATH_SKINNY && path != TI_PATH_GEMM) return TI_ERR_INVALID_ARG;
+  if (path != TI_PATH_AUTO && path != TI_PATH_SKINNY && path != TI_PATH_GEMM && path != TI_PATH_DECODE)
+    return TI_ERR_INVALID_ARG;
   st = check_device();
   if (st != TI_OK) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (path == TI_PATH_DECODE) {
+    if (stage != tinyinfer::kStageBoth) return TI_ERR_UNSUPPORTED;
+    const hipError_t e = tinyinfer::launch_decode_mlp(a, s);
+    if (e == hipErrorNotSupported) return TI_ERR_UNSUPPORTED;
+    return to_status(e);
+  }
   if (path == TI_PATH_AUTO) path = ((size_t)a.n >= kGemmMinTokens) ? TI_PATH_GEMM : TI_PATH_SKINNY;
-  return to_status(path == TI_PATH_GEMM ? tinyinfer::launch_gemm_mlp(a, stage, s)
-                                        : tinyinfer::launch_skinny_mlp(a, stage, s));
+  if (path == TI_PATH_GEMM) return to_status(tinyinfer::launch_gemm_mlp(a, stage, s));
+  // small batches: the streaming kernels where they apply (n <= 8), else the
+  // 16-token-tile skinny kernels
+  if ((size_t)a.n <= kStreamMaxTokens && tinyinfer::stream_supported(a, stage))
+    return to_status(tinyinfer::launch_stream_mlp(a, stage, s));
+  return to_status(tinyinfer::launch_skinny_mlp(a, stage, s));
 }
 
 int64_t as_dim(size_t v) { return v > (size_t)INT64_MAX ? -1 : (int64_t)v; }
@@ -150,10 +170,22 @@ const char* tinyinfer_mxfp4_status_string(int status) {
     case TI_ERR_HIP: return "HIP runtime error";
     case TI_ERR_NO_DEVICE: return "no gfx950 (MI355X) device is current";
     case TI_ERR_TOO_LARGE: return "size exceeds kernel limits";
+    case TI_ERR_MISALIGNED: return "activation, weight and tmp pointers must be 16-byte aligned";
+    case TI_ERR_UNSUPPORTED: return "the requested kernel path does not support this call";
     default: return "unknown status";
   }
 }
 
-int tinyinfer_mxfp4_abi_version(void) { return 2; }
+int tinyinfer_mxfp4_diagnostics(uint32_t* decode_barrier_timeouts) {
+  if (!decode_barrier_timeouts) return TI_ERR_INVALID_ARG;
+  const int st = check_device();
+  if (st != TI_OK) return st;
+  const unsigned int v = tinyinfer::decode_barrier_timeouts();
+  if (v == 0xffffffffu) return TI_ERR_HIP;
+  *decode_barrier_timeouts = v;
+  return TI_OK;
+}
+
+int tinyinfer_mxfp4_abi_version(void) { return 3; }
 
 }  // extern "C"

@@ -69,23 +69,40 @@ __device__ __forceinline__ uint32_t dq_byte_bf16_exact(uint32_t byte, uint32_t b
 }
 
 // 8 codes in one dword (elements 0..7, element 0 in the low nibble) -> 8 bf16
-// as four dwords.  `b` is the e8m0 byte of their block.
-__device__ __forceinline__ u32x4_t dq8_bf16(uint32_t w, uint32_t b) {
+// as four dwords, `b` being the e8m0 byte of their block.
+//
+// dq8_bf16_fast: hardware conversion with the block scale folded in
+// (v_cvt_scalef32_pk_bf16_fp4); exact only when e8m0_fast_ok(b).
+__device__ __forceinline__ u32x4_t dq8_bf16_fast(uint32_t w, uint32_t b) {
   u32x4_t r;
-  if (__builtin_expect(e8m0_fast_ok(b), 1)) {
-    float s = __uint_as_float(b << 23);
-    r.x = bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 0));
-    r.y = bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 1));
-    r.z = bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 2));
-    r.w = bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 3));
-  } else {
-    r.x = dq_byte_bf16_exact(w & 0xffu, b);
-    r.y = dq_byte_bf16_exact((w >> 8) & 0xffu, b);
-    r.z = dq_byte_bf16_exact((w >> 16) & 0xffu, b);
-    r.w = dq_byte_bf16_exact(w >> 24, b);
-  }
+  const float s = __uint_as_float(b << 23);
+  r.x = bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 0));
+  r.y = bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 1));
+  r.z = bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 2));
+  r.w = bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 3));
   return r;
 }
+
+// dq8_bf16_exact: exact for every scale byte (subnormal products, +-inf, NaN).
+__device__ __forceinline__ u32x4_t dq8_bf16_exact(uint32_t w, uint32_t b) {
+  u32x4_t r;
+  r.x = dq_byte_bf16_exact(w & 0xffu, b);
+  r.y = dq_byte_bf16_exact((w >> 8) & 0xffu, b);
+  r.z = dq_byte_bf16_exact((w >> 16) & 0xffu, b);
+  r.w = dq_byte_bf16_exact(w >> 24, b);
+  return r;
+}
+
+// Per-lane choice of the two (for code where lanes' scales are independent).
+// Hot loops instead decide once per wave with wave_all_fast() and call
+// dq8_bf16_fast / dq8_bf16_exact directly: a per-dword branch costs more
+// than the conversion.
+__device__ __forceinline__ u32x4_t dq8_bf16(uint32_t w, uint32_t b) {
+  return __builtin_expect(e8m0_fast_ok(b), 1) ? dq8_bf16_fast(w, b) : dq8_bf16_exact(w, b);
+}
+
+// True (uniformly across the wave) when every active lane's flag is true.
+__device__ __forceinline__ bool wave_all(bool ok) { return !__any(!ok); }
 
 // 8 codes -> 8 fp32 (exact, all scale bytes).
 __device__ __forceinline__ void dq8_f32(uint32_t w, uint32_t b, float* out) {

@@ -35,6 +35,22 @@ hipError_t launch_skinny_mlp(const MlpArgs& a, int stage, hipStream_t stream);
 // Tiled MFMA GEMM path (n >= 128 preferred; any n >= 1 is correct).
 hipError_t launch_gemm_mlp(const MlpArgs& a, int stage, hipStream_t stream);
 
+// Streaming decode GEMV kernels (n <= 8): one launch per stage, contiguous
+// load front across the chip.  stream_supported() says whether the call's
+// shape, alignment and LDS needs fit; launch_stream_mlp must only be called
+// when it does.
+bool stream_supported(const MlpArgs& a, int stage);
+hipError_t launch_stream_mlp(const MlpArgs& a, int stage, hipStream_t stream);
+
+// Fused persistent decode kernel (gate_up, grid barrier, down in one launch)
+// for n <= 8 tokens; hipErrorNotSupported when the shape, alignment or the
+// device's LDS/occupancy do not allow it (the caller then uses the skinny path).
+hipError_t launch_decode_mlp(const MlpArgs& a, hipStream_t stream);
+
+// Grid-barrier spin timeouts of the fused decode kernel since load (0 unless a
+// workgroup was not resident); synchronous.
+unsigned int decode_barrier_timeouts();
+
 hipError_t launch_dequant(const uint8_t* packed, const uint8_t* scale, int64_t rows, int64_t k,
                           void* out, int out_dtype, hipStream_t stream);
 

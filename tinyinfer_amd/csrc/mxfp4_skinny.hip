@@ -51,48 +51,15 @@ __device__ __forceinline__ void load_x_chunk(const uint16_t* __restrict__ x, int
   }
 }
 
-// One batch of a wave's work: rows [row0, row0+16) of W, K chunks [c0, c1),
-// c1 - c0 <= NCH.
-template <int DT, int T, int NCH>
-__device__ __forceinline__ void wave_batch(const uint16_t* __restrict__ x, const uint8_t* __restrict__ w,
-                                            const uint8_t* __restrict__ ws, int64_t m_base, int64_t M,
-                                            int64_t K, int64_t R, int64_t row0, int c0, int c1,
-                                            f32x4_t (&acc)[T]) {
+// MFMA part of a batch: dequantize chunk u's four dwords and multiply them
+// into the token tiles, activations fetched one chunk ahead.
+template <int DT, int T, int NCH, bool FAST>
+__device__ __forceinline__ void batch_mfma(const uint16_t* __restrict__ x, int64_t m_base, int64_t M,
+                                           int64_t K, int c0, int c1, const u32x4_t (&wv)[NCH],
+                                           const uint32_t (&sb)[NCH], f32x4_t (&acc)[T]) {
   const int lane = threadIdx.x & 63;
   const int r = lane & 15;
   const int q = lane >> 4;
-  // R is a multiple of 32 (checked at the C ABI), so every row of the tile exists.
-  const uint8_t* wrow = w + (row0 + r) * (K / 2) + 16 * q;
-  const uint8_t* srow = ws + (row0 + r) * (K / 32) + q;
-
-  // 1. every weight and scale load of this wave, back to back
-  u32x4_t wv[NCH];
-  uint32_t sb[NCH];
-  if (c1 - c0 == NCH && (int64_t)c1 * kChunkK <= K) {
-    // whole batch in bounds: unpredicated loads at immediate offsets
-    const uint8_t* wp = wrow + (int64_t)c0 * (kChunkK / 2);
-    const uint8_t* sp = srow + (int64_t)c0 * (kChunkK / 32);
-#pragma unroll
-    for (int u = 0; u < NCH; ++u)
-      wv[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wp + u * (kChunkK / 2)));
-#pragma unroll
-    for (int u = 0; u < NCH; ++u) sb[u] = sp[u * (kChunkK / 32)];
-  } else {
-#pragma unroll
-    for (int u = 0; u < NCH; ++u) {
-      const int64_t k0 = (int64_t)(c0 + u) * kChunkK + 32 * q;
-      const bool ok = (c0 + u < c1) && (k0 < K);
-      wv[u] = u32x4_t{0u, 0u, 0u, 0u};
-      sb[u] = 127u;
-      if (ok) {
-        wv[u] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4_t*>(wrow + (int64_t)(c0 + u) * (kChunkK / 2)));
-        sb[u] = srow[(int64_t)(c0 + u) * (kChunkK / 32)];
-      }
-    }
-  }
-
-  // 2. activations one chunk ahead, then dequant + MFMA
   auto chunk_ok = [&](int u, int64_t& k0) {
     k0 = (int64_t)(c0 + u) * kChunkK + 32 * q;
     return (c0 + u < c1) && (k0 < K);
@@ -100,7 +67,7 @@ __device__ __forceinline__ void wave_batch(const uint16_t* __restrict__ x, const
   auto compute = [&](int u, const u32x4_t (&xc)[T * 4]) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const u32x4_t a = dq8_bf16(wv[u][t], sb[u]);
+      const u32x4_t a = FAST ? dq8_bf16_fast(wv[u][t], sb[u]) : dq8_bf16_exact(wv[u][t], sb[u]);
 #pragma unroll
       for (int tt = 0; tt < T; ++tt) {
         if constexpr (DT == kBF16) {
@@ -133,14 +100,93 @@ __device__ __forceinline__ void wave_batch(const uint16_t* __restrict__ x, const
   }
 }
 
+// Whole batch in bounds and the scale rows 16-byte aligned: straight-line
+// code, so the compiler can wait for exactly the loads each step needs.
+// The batch's scale bytes (16 rows x 4*NCH) are fetched first with one
+// coalesced 16-byte load per lane into the wave's private LDS slice `sl`,
+// then every weight load is issued, then the slice is read back per lane.
+template <int DT, int T, int NCH>
+__device__ __forceinline__ void batch_fast(const uint16_t* __restrict__ x, const uint8_t* __restrict__ w,
+                                           const uint8_t* __restrict__ ws, int64_t m_base, int64_t M,
+                                           int64_t K, int64_t row0, int c0, f32x4_t (&acc)[T],
+                                           uint8_t* sl) {
+  constexpr int kSRow = 4 * NCH;                 // scale bytes per row per batch
+  constexpr int kPieces = kSRow / 16;            // 16-byte pieces per row
+  static_assert(kSRow % 16 == 0, "NCH must be a multiple of 4");
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15;
+  const int q = lane >> 4;
+  const int s_row = lane / kPieces, s_piece = lane % kPieces;
+  u32x4_t sp = {0u, 0u, 0u, 0u};
+  if (lane < 16 * kPieces)
+    sp = *reinterpret_cast<const u32x4_t*>(ws + (row0 + s_row) * (K / 32) + (int64_t)c0 * 4 + 16 * s_piece);
+  // R is a multiple of 32 (checked at the C ABI), so every row of the tile exists.
+  const uint8_t* wp = w + (row0 + r) * (K / 2) + 16 * q + (int64_t)c0 * (kChunkK / 2);
+  u32x4_t wv[NCH];
+#pragma unroll
+  for (int u = 0; u < NCH; ++u)
+    wv[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wp + u * (kChunkK / 2)));
+  if (lane < 16 * kPieces) *reinterpret_cast<u32x4_t*>(sl + s_row * kSRow + 16 * s_piece) = sp;
+  // other lanes' bytes are read back: keep the reads after the writes
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  uint32_t sb[NCH];
+  bool ok = true;
+#pragma unroll
+  for (int u = 0; u < NCH; ++u) {
+    sb[u] = sl[r * kSRow + 4 * u + q];
+    ok = ok && e8m0_fast_ok(sb[u]);
+  }
+  if (wave_all(ok)) batch_mfma<DT, T, NCH, true>(x, m_base, M, K, c0, c0 + NCH, wv, sb, acc);
+  else batch_mfma<DT, T, NCH, false>(x, m_base, M, K, c0, c0 + NCH, wv, sb, acc);
+}
+
+// Any batch (partial K tail, unaligned scales): predicated loads, scale bytes
+// straight from global memory.
+template <int DT, int T, int NCH>
+__device__ __forceinline__ void batch_generic(const uint16_t* __restrict__ x, const uint8_t* __restrict__ w,
+                                              const uint8_t* __restrict__ ws, int64_t m_base, int64_t M,
+                                              int64_t K, int64_t row0, int c0, int c1, f32x4_t (&acc)[T]) {
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15;
+  const int q = lane >> 4;
+  const uint8_t* wrow = w + (row0 + r) * (K / 2) + 16 * q;
+  const uint8_t* srow = ws + (row0 + r) * (K / 32) + q;
+  u32x4_t wv[NCH];
+  uint32_t sb[NCH];
+#pragma unroll
+  for (int u = 0; u < NCH; ++u) {
+    const int64_t k0 = (int64_t)(c0 + u) * kChunkK + 32 * q;
+    const bool in = (c0 + u < c1) && (k0 < K);
+    wv[u] = u32x4_t{0u, 0u, 0u, 0u};
+    sb[u] = 127u;
+    if (in) {
+      wv[u] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4_t*>(wrow + (int64_t)(c0 + u) * (kChunkK / 2)));
+      sb[u] = srow[(int64_t)(c0 + u) * (kChunkK / 32)];
+    }
+  }
+  bool ok = true;
+#pragma unroll
+  for (int u = 0; u < NCH; ++u) ok = ok && e8m0_fast_ok(sb[u]);
+  if (wave_all(ok)) batch_mfma<DT, T, NCH, true>(x, m_base, M, K, c0, c1, wv, sb, acc);
+  else batch_mfma<DT, T, NCH, false>(x, m_base, M, K, c0, c1, wv, sb, acc);
+}
+
 // A wave's whole K slice [c0, c1), in batches of NCH chunks.
 template <int DT, int T, int NCH>
 __device__ __forceinline__ void wave_skinny(const uint16_t* __restrict__ x, const uint8_t* __restrict__ w,
                                             const uint8_t* __restrict__ ws, int64_t m_base, int64_t M,
                                             int64_t K, int64_t R, int64_t row0, int c0, int c1,
-                                            f32x4_t (&acc)[T]) {
-  for (int cb = c0; cb < c1; cb += NCH)
-    wave_batch<DT, T, NCH>(x, w, ws, m_base, M, K, R, row0, cb, cb + NCH < c1 ? cb + NCH : c1, acc);
+                                            f32x4_t (&acc)[T], uint8_t* sl) {
+  (void)R;
+  const bool aligned = ((K / 32) % 16 == 0) && ((reinterpret_cast<uintptr_t>(ws) & 15u) == 0);
+  for (int cb = c0; cb < c1; cb += NCH) {
+    const int ce = cb + NCH < c1 ? cb + NCH : c1;
+    if (aligned && ce - cb == NCH && cb % 4 == 0 && (int64_t)ce * kChunkK <= K)
+      batch_fast<DT, T, NCH>(x, w, ws, m_base, M, K, row0, cb, acc, sl);
+    else
+      batch_generic<DT, T, NCH>(x, w, ws, m_base, M, K, row0, cb, ce, acc);
+  }
 }
 
 // GATEUP: out = h[M, R] = SiLU(x W0^T) * (x W1^T), K = hidden, R = inter.
@@ -155,6 +201,7 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(const uint16_t* __restr
                                                          uint16_t* __restrict__ out) {
   constexpr int KS = GATEUP ? NW / 2 : NW;   // K slices
   __shared__ f32x4_t red[NW][T][64];
+  __shared__ __attribute__((aligned(16))) uint8_t scale_slices[NW][16 * 4 * NCH];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int mat = GATEUP ? (wave & 1) : 0;
@@ -168,7 +215,8 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(const uint16_t* __restr
   f32x4_t acc[T];
 #pragma unroll
   for (int tt = 0; tt < T; ++tt) acc[tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  wave_skinny<DT, T, NCH>(x, mat ? w1 : w0, mat ? s1 : s0, m_base, M, K, R, row0, c0, c1, acc);
+  wave_skinny<DT, T, NCH>(x, mat ? w1 : w0, mat ? s1 : s0, m_base, M, K, R, row0, c0, c1, acc,
+                          scale_slices[wave]);
 
 #pragma unroll
   for (int tt = 0; tt < T; ++tt) red[wave][tt][lane] = acc[tt];
