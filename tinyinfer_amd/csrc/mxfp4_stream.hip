@@ -4,19 +4,26 @@
 // mlp_stage1_mxfp4 / mlp_stage2_mxfp4 (tinyinfer/csrc/mlp_fp4.cu:79-142,
 // 365-426): gate_up with the SiLU*up epilogue writes h, down writes out.
 //
-// Memory order is what decides HBM efficiency at this size, so the work is
-// laid out around the load stream:
+// Memory order is what decides HBM efficiency here, so the work is laid out
+// around the load stream (each choice measured on MI355X with load-only
+// probes of the same instruction shapes):
 //   * an item is 8 weight rows x 128 contiguous bytes (256 K elements): one
 //     dwordx4 load per lane, 8 full cache lines per instruction;
-//   * a row group is 8 rows x all of K (x both matrices for gate_up); the
-//     waves of a workgroup share a row group's items, and workgroup g takes
-//     row groups g, g+G, g+2G, ...: at any moment the whole chip reads one
-//     contiguous band of each matrix;
-//   * each wave keeps the next row group's items in flight (double buffer)
-//     while it multiplies the current one; per row group one LDS reduction
-//     over the waves, then the epilogue.
-// x is staged in LDS once per workgroup (issued after the first row group's
-// weight loads, so its latency overlaps them).
+//   * a row group is 8 rows x all of K (x both matrices for gate_up).
+//     Workgroup g takes row groups g, g+G, g+2G, ... and each of its waves a
+//     contiguous run of the row group's K segments, so the whole chip reads
+//     one contiguous band of each matrix at a time;
+//   * one 8-wave workgroup per CU, each wave with its next row group's loads
+//     in flight while it multiplies the current one (8 waves/CU streaming a
+//     few loads each gave the highest bandwidth; more waves gave less);
+//   * no workgroup barrier in the stream: a wave stores its partial sums in
+//     an LDS slot of the row group and bumps an LDS counter; the last wave to
+//     finish a row group sums the slots in a fixed order (bit-reproducible)
+//     and runs the epilogue;
+//   * a wave fetches the e8m0 scale bytes of its segments with one 8-byte load
+//     per (row, segment) ahead of its weights and stages them in its own LDS
+//     area (a scale-byte load per weight instruction costs ~20% bandwidth).
+// x is staged in LDS once per workgroup, after the first row groups' loads.
 //
 // MFMA mapping ("8 rows x 128 B"): lane l holds weight row l&7, 32-element K
 // block l>>3 of the item.  With these as the A operand of
@@ -31,7 +38,9 @@ namespace tinyinfer {
 namespace {
 
 constexpr int kNW = 8;            // waves per workgroup
-constexpr int kItemK = 256;       // K elements per item
+constexpr int kItemK = 256;       // K elements per item (one 128-byte segment per row)
+constexpr int kMaxSpw = 8;        // max segments per wave per matrix (more would spill)
+constexpr int kSclPerWave = 2 * 8 * kMaxSpw * 8;   // wave-private scale bytes (mats x rows x segs x 8)
 
 struct StreamArgs {
   const uint16_t* x;      // [M, K] activations (x for gate_up, h for down)
@@ -42,99 +51,128 @@ struct StreamArgs {
   uint16_t* out;          // [M, R]
   int M, K, R;
   int segs;               // K / kItemK
-  int items;              // items per row group: mats * segs
-  int ipw;                // items per wave per row group: ceil(items / kNW)
   int rgroups;            // R / 8
+  int nrg_max;            // max row groups per workgroup
   int xs_stride;          // bytes per staged token row
+  int lds_scl, lds_red, lds_cnt;   // LDS byte offsets
 };
 
-// Issue one row group's items for this wave (IPWMAX loads + scale bytes,
-// always the same number of instructions: past-the-end items read the
-// matrix's first 16 bytes and are not multiplied).
-template <int IPWMAX, bool GATEUP>
-__device__ __forceinline__ void issue_rg(const StreamArgs& a, int rg, int wave, u32x4_t (&wv)[IPWMAX],
-                                         uint32_t (&sb)[IPWMAX]) {
+// Wave w's segment run [lo, hi) of a row group (same for both matrices).
+__device__ __forceinline__ void seg_run(const StreamArgs& a, int wave, int& lo, int& hi) {
+  lo = a.segs * wave / kNW;
+  hi = a.segs * (wave + 1) / kNW;
+}
+
+// A row group's loads for this wave: scale bytes (8-byte pieces, one per
+// (matrix, row, segment), SPL per lane) first, then the weight items
+// (matrix-major, then segment).  A fixed instruction count: unused slots read
+// the matrices' first bytes and are not used.
+template <int SPW, bool GATEUP, int SPL>
+__device__ __forceinline__ void issue_rg(const StreamArgs& a, int rg, int wave,
+                                         u32x4_t (&wv)[(GATEUP ? 2 : 1) * SPW], u32x2_t (&sc)[SPL]) {
+  constexpr int kMats = GATEUP ? 2 : 1;
   const int lane = threadIdx.x & 63;
   const int r8 = lane & 7, q8 = lane >> 3;
+  int lo, hi;
+  seg_run(a, wave, lo, hi);
+  const int n = hi - lo;
+  const int nn = n > 0 ? n : 1;
   const bool rg_ok = rg < a.rgroups;
-  const int64_t row = (int64_t)(rg_ok ? rg : 0) * 8 + r8;
+  const int64_t rgc = rg_ok ? rg : 0;
 #pragma unroll
-  for (int k = 0; k < IPWMAX; ++k) {
-    const int item = wave + kNW * k;
-    const bool ok = rg_ok && k < a.ipw && item < a.items;
-    const int mat = GATEUP ? (item >= a.segs) : 0;
-    const int seg = item - mat * a.segs;
-    const uint8_t* w = mat ? a.w1 : a.w0;
+  for (int i = 0; i < SPL; ++i) {
+    const int p = lane + 64 * i;                 // piece (mat, row, seg): p = (mat * 8 + row) * n + seg
+    const bool ok = rg_ok && p < kMats * 8 * n;
+    const int pc = ok ? p : 0;
+    const int mr = pc / nn, sg = pc - mr * nn;
+    const int mat = GATEUP ? mr / 8 : 0;
+    const int row = mr - mat * 8;
     const uint8_t* s = mat ? a.s1 : a.s0;
-    const uint8_t* wp = ok ? w + row * (a.K / 2) + seg * (kItemK / 2) + 16 * q8 : a.w0;
-    const uint8_t* sp = ok ? s + row * (a.K / 32) + seg * (kItemK / 32) + q8 : a.s0;
+    const uint8_t* sp = ok ? s + (rgc * 8 + row) * (a.K / 32) + (int64_t)(lo + sg) * 8 : a.s0;
+    sc[i] = *reinterpret_cast<const u32x2_t*>(sp);
+  }
+  const int64_t row = rgc * 8 + r8;
+#pragma unroll
+  for (int k = 0; k < kMats * SPW; ++k) {
+    const int mat = GATEUP ? k / SPW : 0;
+    const int sg = k - mat * SPW;
+    const bool ok = rg_ok && sg < n;
+    const uint8_t* w = mat ? a.w1 : a.w0;
+    const uint8_t* wp = ok ? w + row * (a.K / 2) + (int64_t)(lo + sg) * (kItemK / 2) + 16 * q8 : a.w0;
     wv[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wp));
-    sb[k] = *sp;
   }
 }
 
-// Multiply one row group's items; partial sums per matrix into acc[mat].
-// FAST: every scale byte of the items is in the range where the hardware
-// conversion is exact.  The choice is made once per row group outside this
-// body, so each conversion sits in the same basic block as the MFMA that
-// consumes it.
-template <int DT, int IPWMAX, bool GATEUP, bool FAST>
-__device__ __forceinline__ void compute_body(const StreamArgs& a, int wave, const u32x4_t (&wv)[IPWMAX],
-                                             const uint32_t (&sb)[IPWMAX], const uint8_t* xrow,
-                                             f32x4_t (&acc)[2]) {
-  const int lane = threadIdx.x & 63;
-  const int q8 = lane >> 3;
+// Multiply this wave's items of one row group (FAST: every scale byte in the
+// hardware-exact range; chosen once outside this body so each conversion
+// sits in the same basic block as its MFMA).
+template <int DT, int SPW, bool GATEUP, bool FAST>
+__device__ __forceinline__ void mma_items(int n, int lo, const u32x4_t (&wv)[(GATEUP ? 2 : 1) * SPW],
+                                          const uint32_t (&sb)[(GATEUP ? 2 : 1) * SPW], const uint8_t* xrow,
+                                          f32x4_t (&acc)[2]) {
+  constexpr int kMats = GATEUP ? 2 : 1;
+  const int q8 = (threadIdx.x & 63) >> 3;
 #pragma unroll
-  for (int k = 0; k < IPWMAX; ++k) {
-    const int item = wave + kNW * k;
-    if (k >= a.ipw || item >= a.items) break;            // wave-uniform
-    const int mat = GATEUP ? (item >= a.segs) : 0;
-    const int seg = item - mat * a.segs;
-    const int kx = seg * kItemK + 32 * q8;
+  for (int mat = 0; mat < kMats; ++mat) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const u32x4_t wa = FAST ? dq8_bf16_fast(wv[k][t], sb[k]) : dq8_bf16_exact(wv[k][t], sb[k]);
-      const u32x4_t xb = *reinterpret_cast<const u32x4_t*>(xrow + 2 * (kx + 8 * t));
-      // uniform branch on the matrix (a runtime index into acc would spill it)
-      if (GATEUP && mat) {
+    for (int sg = 0; sg < SPW; ++sg) {
+      if (sg >= n) break;                                   // wave-uniform
+      const int k = mat * SPW + sg;
+      const int kx = (lo + sg) * kItemK + 32 * q8;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const u32x4_t wa = FAST ? dq8_bf16_fast(wv[k][t], sb[k]) : dq8_bf16_exact(wv[k][t], sb[k]);
+        const u32x4_t xb = *reinterpret_cast<const u32x4_t*>(xrow + 2 * (kx + 8 * t));
         if constexpr (DT == kBF16) {
-          acc[1] = mfma16x16x32(wa, xb, acc[1]);
+          acc[mat] = mfma16x16x32(wa, xb, acc[mat]);
         } else {
-          u32x4_t hi, lo;
-          f16x8_split_bf16(xb, hi, lo);
-          acc[1] = mfma16x16x32(wa, lo, mfma16x16x32(wa, hi, acc[1]));
-        }
-      } else {
-        if constexpr (DT == kBF16) {
-          acc[0] = mfma16x16x32(wa, xb, acc[0]);
-        } else {
-          u32x4_t hi, lo;
-          f16x8_split_bf16(xb, hi, lo);
-          acc[0] = mfma16x16x32(wa, lo, mfma16x16x32(wa, hi, acc[0]));
+          u32x4_t xh, xl;
+          f16x8_split_bf16(xb, xh, xl);
+          acc[mat] = mfma16x16x32(wa, xl, mfma16x16x32(wa, xh, acc[mat]));
         }
       }
     }
   }
 }
 
-template <int DT, int IPWMAX, bool GATEUP>
-__device__ __forceinline__ void compute_rg(const StreamArgs& a, int wave, const u32x4_t (&wv)[IPWMAX],
-                                           const uint32_t (&sb)[IPWMAX], const uint8_t* xs,
+template <int DT, int SPW, bool GATEUP, int SPL>
+__device__ __forceinline__ void compute_rg(const StreamArgs& a, int wave,
+                                           const u32x4_t (&wv)[(GATEUP ? 2 : 1) * SPW],
+                                           const u32x2_t (&sc)[SPL], uint8_t* my_scl, const uint8_t* xs,
                                            f32x4_t (&acc)[2]) {
+  constexpr int kMats = GATEUP ? 2 : 1;
   const int lane = threadIdx.x & 63;
+  const int r8 = lane & 7, q8 = lane >> 3;
+  int lo, hi;
+  seg_run(a, wave, lo, hi);
+  const int n = hi - lo;
+  // stage this wave's scale pieces ([mat][row][seg] x 8 bytes) and read back
+  // the byte of each of this lane's items
+#pragma unroll
+  for (int i = 0; i < SPL; ++i) {
+    const int p = lane + 64 * i;
+    if (p < kMats * 8 * n) *reinterpret_cast<u32x2_t*>(my_scl + 8 * p) = sc[i];
+  }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");   // other lanes' bytes are read back
+  uint32_t sb[kMats * SPW];
+  bool ok = true;
+#pragma unroll
+  for (int k = 0; k < kMats * SPW; ++k) {
+    const int mat = GATEUP ? k / SPW : 0;
+    const int sg = k - mat * SPW;
+    sb[k] = sg < n ? (uint32_t)my_scl[8 * ((mat * 8 + r8) * n + sg) + q8] : 127u;
+    ok = ok && e8m0_fast_ok(sb[k]);
+  }
   const int c = lane & 15;
   const int tok = (c & 7) < a.M ? (c & 7) : a.M - 1;     // columns >= M are discarded
   const uint8_t* xrow = xs + tok * a.xs_stride;
   acc[0] = acc[1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  bool ok = true;
-#pragma unroll
-  for (int k = 0; k < IPWMAX; ++k) ok = ok && (k >= a.ipw || e8m0_fast_ok(sb[k]));
-  if (wave_all(ok)) compute_body<DT, IPWMAX, GATEUP, true>(a, wave, wv, sb, xrow, acc);
-  else compute_body<DT, IPWMAX, GATEUP, false>(a, wave, wv, sb, xrow, acc);
+  if (wave_all(ok)) mma_items<DT, SPW, GATEUP, true>(n, lo, wv, sb, xrow, acc);
+  else mma_items<DT, SPW, GATEUP, false>(n, lo, wv, sb, xrow, acc);
 }
 
 // Fold C[r][t] + C[r+8][t+8] and store this wave's partial (rows 4g..4g+3,
-// token t) for matrix `mat` into LDS.
+// token t) into LDS.
 __device__ __forceinline__ void store_partial(const f32x4_t& acc, float* red, int M) {
   const int lane = threadIdx.x & 63;
   f32x4_t part;
@@ -144,22 +182,25 @@ __device__ __forceinline__ void store_partial(const f32x4_t& acc, float* red, in
   if (c < 8 && g < 2 && c < M) *reinterpret_cast<f32x4_t*>(red + c * 8 + 4 * g) = part;
 }
 
-template <int DT, int IPWMAX, bool GATEUP>
-__global__ __launch_bounds__(kNW * 64, 2) void stream_kernel(StreamArgs a) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+template <int DT, int SPW, bool GATEUP, int SPL>
+__global__ __launch_bounds__(kNW * 64, 1) void stream_kernel(StreamArgs a) {
   constexpr int kMats = GATEUP ? 2 : 1;
-  // LDS: [x staging M rows][partials 2 parities x kNW waves x kMats x 64 floats]
-  float* red = reinterpret_cast<float*>(lds + a.M * a.xs_stride);
+  constexpr int kItems = kMats * SPW;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
   const int G = gridDim.x;
   const int g = blockIdx.x;
+  uint8_t* my_scl = lds + a.lds_scl + wave * kSclPerWave;
+  float* red = reinterpret_cast<float*>(lds + a.lds_red);                   // [nrg_max][kNW][kMats][64]
+  unsigned int* cnt = reinterpret_cast<unsigned int*>(lds + a.lds_cnt);    // [nrg_max]
 
-  u32x4_t wa[IPWMAX], wb[IPWMAX];
-  uint32_t sa[IPWMAX], sb2[IPWMAX];
-  issue_rg<IPWMAX, GATEUP>(a, g, wave, wa, sa);
+  u32x4_t wa[kItems], wb[kItems];
+  u32x2_t sca[SPL], scb[SPL];
+  issue_rg<SPW, GATEUP, SPL>(a, g, wave, wa, sca);
+  issue_rg<SPW, GATEUP, SPL>(a, g + G, wave, wb, scb);
 
-  // stage x [M, K] (after the first weight loads: its latency overlaps them),
-  // four 16-byte loads in flight per thread per round
+  // stage x [M, K] and clear the row-group counters
   {
     constexpr int kB = 4;
     const int per_row = a.K / 8;
@@ -182,39 +223,46 @@ __global__ __launch_bounds__(kNW * 64, 2) void stream_kernel(StreamArgs a) {
         }
       }
     }
+    for (int i = threadIdx.x; i < a.nrg_max; i += kNW * 64) cnt[i] = 0u;
   }
   __syncthreads();
 
-  int parity = 0;
-  auto finish_rg = [&](int rg, const f32x4_t (&acc)[2]) {
-    float* slot = red + parity * (kNW * kMats * 64);
+  // after a row group: partials into its slot, count, and the last wave of
+  // the workgroup to get here runs the epilogue
+  auto finish_rg = [&](int rg, int li, const f32x4_t (&acc)[2]) {
+    float* slot = red + (int64_t)li * (kNW * kMats * 64);
 #pragma unroll
     for (int m = 0; m < kMats; ++m) store_partial(acc[m], slot + (wave * kMats + m) * 64, a.M);
-    __syncthreads();
-    // epilogue: 8 rows x M tokens, fixed-order sum over the waves
-    const int n = 8 * a.M;
-    for (int e = threadIdx.x; e < n; e += kNW * 64) {
-      const int t = e >> 3, r = e & 7;
-      float y0 = 0.f, y1 = 0.f;
-      for (int w = 0; w < kNW; ++w) {
-        y0 += slot[(w * kMats + 0) * 64 + t * 8 + r];
-        if (GATEUP) y1 += slot[(w * kMats + 1) * 64 + t * 8 + r];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    unsigned int old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(&cnt[li], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+    old = __shfl(old, 0, 64);
+    if (old == kNW - 1) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      // epilogue: 8 rows x M tokens, one lane each, fixed-order sum over the waves
+      if (lane < 8 * a.M) {
+        const int t = lane >> 3, r = lane & 7;
+        float y0 = 0.f, y1 = 0.f;
+        for (int w = 0; w < kNW; ++w) {
+          y0 += slot[(w * kMats + 0) * 64 + t * 8 + r];
+          if (GATEUP) y1 += slot[(w * kMats + 1) * 64 + t * 8 + r];
+        }
+        const float v = GATEUP ? silu_f32(y0) * y1 : y0;
+        a.out[(int64_t)t * a.R + rg * 8 + r] = f32_to_act<DT>(v);
       }
-      const float v = GATEUP ? silu_f32(y0) * y1 : y0;
-      a.out[(int64_t)t * a.R + rg * 8 + r] = f32_to_act<DT>(v);
     }
-    parity ^= 1;
   };
 
-  for (int rg = g; rg < a.rgroups; rg += 2 * G) {
+  int li = 0;
+  for (int rg = g; rg < a.rgroups; rg += 2 * G, li += 2) {
     f32x4_t acc[2];
-    issue_rg<IPWMAX, GATEUP>(a, rg + G, wave, wb, sb2);
-    compute_rg<DT, IPWMAX, GATEUP>(a, wave, wa, sa, lds, acc);
-    finish_rg(rg, acc);
+    compute_rg<DT, SPW, GATEUP, SPL>(a, wave, wa, sca, my_scl, lds, acc);
+    issue_rg<SPW, GATEUP, SPL>(a, rg + 2 * G, wave, wa, sca);
+    finish_rg(rg, li, acc);
     if (rg + G >= a.rgroups) break;
-    issue_rg<IPWMAX, GATEUP>(a, rg + 2 * G, wave, wa, sa);
-    compute_rg<DT, IPWMAX, GATEUP>(a, wave, wb, sb2, lds, acc);
-    finish_rg(rg + G, acc);
+    compute_rg<DT, SPW, GATEUP, SPL>(a, wave, wb, scb, my_scl, lds, acc);
+    issue_rg<SPW, GATEUP, SPL>(a, rg + 3 * G, wave, wb, scb);
+    finish_rg(rg + G, li + 1, acc);
   }
 }
 
@@ -241,10 +289,35 @@ DevCaps caps() {
   return cache[dev];
 }
 
-// One workgroup per row group up to what is resident at once (a second
-// round of workgroups would restart the load stream).
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Geometry of one stage; false when the streaming kernel does not apply.
+bool plan(int64_t M, int64_t K, int64_t R, bool gateup, const DevCaps& d, StreamArgs& a, int& grid,
+          int64_t& lds) {
+  if (d.cus < 1 || M < 1 || M > 8 || K % kItemK != 0 || R % 8 != 0) return false;
+  if (K > (1 << 20) || R > (1 << 24)) return false;
+  const int mats = gateup ? 2 : 1;
+  a.M = (int)M;
+  a.K = (int)K;
+  a.R = (int)R;
+  a.segs = (int)(K / kItemK);
+  const int spw = (a.segs + kNW - 1) / kNW;
+  if (spw > (gateup ? kMaxSpw / 2 : kMaxSpw)) return false;   // double-buffered items fit in VGPRs
+  if (mats * 8 * spw > 64) return false;             // scale pieces: one per lane
+  a.rgroups = (int)(R / 8);
+  grid = d.cus < a.rgroups ? d.cus : a.rgroups;
+  a.nrg_max = (a.rgroups + grid - 1) / grid;
+  a.xs_stride = (int)(2 * K + 16);
+  a.lds_scl = (int)(M * a.xs_stride);
+  a.lds_red = a.lds_scl + kNW * kSclPerWave;
+  a.lds_cnt = a.lds_red + a.nrg_max * kNW * mats * 64 * 4;
+  lds = a.lds_cnt + 4 * ((a.nrg_max + 3) & ~3);
+  return lds <= d.max_lds;
+}
+
 template <int DT, bool GATEUP>
-hipError_t launch(StreamArgs a, size_t lds, int cus, hipStream_t st) {
+hipError_t launch(const StreamArgs& a, int64_t lds, int grid, hipStream_t st) {
+  const int spw = (a.segs + kNW - 1) / kNW;
   auto go = [&](auto kern) -> hipError_t {
     if (lds > 64 * 1024 &&
         hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -252,61 +325,53 @@ hipError_t launch(StreamArgs a, size_t lds, int cus, hipStream_t st) {
       (void)hipGetLastError();
       return hipErrorNotSupported;
     }
-    int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kNW * 64, lds) != hipSuccess) {
-      (void)hipGetLastError();
-      per_cu = 1;
-    }
-    if (per_cu < 1) per_cu = 1;
-    if (per_cu > 2) per_cu = 2;
-    int grid = per_cu * cus;
-    if (grid > a.rgroups) grid = a.rgroups;
-    kern<<<grid, kNW * 64, lds, st>>>(a);
+    kern<<<grid, kNW * 64, (size_t)lds, st>>>(a);
     return hipGetLastError();
   };
-  if (a.ipw <= 2) return go(stream_kernel<DT, 2, GATEUP>);
-  if (a.ipw <= 4) return go(stream_kernel<DT, 4, GATEUP>);
-  if (a.ipw <= 6) return go(stream_kernel<DT, 6, GATEUP>);
-  return go(stream_kernel<DT, 8, GATEUP>);
+  if (spw <= 2) return go(stream_kernel<DT, 2, GATEUP, 1>);
+  if (GATEUP || spw <= 4) return go(stream_kernel<DT, 4, GATEUP, 1>);
+  return go(stream_kernel<DT, 8, false, 1>);
 }
-
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 template <int DT, bool GATEUP>
 hipError_t run_stage(const uint16_t* x, const uint8_t* w0, const uint8_t* s0, const uint8_t* w1,
                      const uint8_t* s1, int64_t M, int64_t K, int64_t R, uint16_t* out, hipStream_t st) {
-  const DevCaps d = caps();
-  if (d.cus < 1 || M < 1 || M > 8 || K % kItemK != 0 || R % 8 != 0) return hipErrorNotSupported;
-  if (K > (1 << 20) || R > (1 << 24)) return hipErrorNotSupported;
-  if (!aligned16(x) || !aligned16(w0) || (GATEUP && !aligned16(w1))) return hipErrorNotSupported;
   StreamArgs a;
+  int grid = 0;
+  int64_t lds = 0;
+  if (!plan(M, K, R, GATEUP, caps(), a, grid, lds)) return hipErrorNotSupported;
   a.x = x;
   a.w0 = w0;
   a.s0 = s0;
   a.w1 = GATEUP ? w1 : w0;
   a.s1 = GATEUP ? s1 : s0;
   a.out = out;
-  a.M = (int)M;
-  a.K = (int)K;
-  a.R = (int)R;
-  a.segs = (int)(K / kItemK);
-  a.items = (GATEUP ? 2 : 1) * a.segs;
-  a.ipw = (a.items + kNW - 1) / kNW;
-  if (a.ipw > 8) return hipErrorNotSupported;
-  a.rgroups = (int)(R / 8);
-  a.xs_stride = (int)(2 * K + 16);
-  const int64_t lds = M * a.xs_stride + 2 * (int64_t)kNW * (GATEUP ? 2 : 1) * 64 * 4;
-  if (lds > d.max_lds) return hipErrorNotSupported;
-  return launch<DT, GATEUP>(a, (size_t)lds, d.cus, st);
+  return launch<DT, GATEUP>(a, lds, grid, st);
 }
 
 }  // namespace
+
+bool stream_supported(const MlpArgs& a, int stage) {
+  const DevCaps d = caps();
+  StreamArgs sa;
+  int grid = 0;
+  int64_t lds = 0;
+  if ((stage & kStageGateUp) && !plan(a.n, a.hidden, a.inter, true, d, sa, grid, lds)) return false;
+  if ((stage & kStageDown) && !plan(a.n, a.inter, a.hidden, false, d, sa, grid, lds)) return false;
+  // 16-byte loads of activations and weights, 8-byte loads of scale bytes
+  const void* p16[] = {a.x, a.gate, a.up, a.down, a.tmp};
+  for (const void* p : p16)
+    if (p && !aligned16(p)) return false;
+  const void* p8[] = {a.gate_scale, a.up_scale, a.down_scale};
+  for (const void* p : p8)
+    if (p && (reinterpret_cast<uintptr_t>(p) & 7u)) return false;
+  return true;
+}
 
 hipError_t launch_stream_mlp(const MlpArgs& a, int stage, hipStream_t st) {
   const uint16_t* x = static_cast<const uint16_t*>(a.x);
   uint16_t* h = static_cast<uint16_t*>(a.tmp);
   uint16_t* y = static_cast<uint16_t*>(a.out);
-  // both stages must be supported before anything is launched
   const bool bf = a.dtype == kBF16;
   if (stage & kStageGateUp) {
     const hipError_t e = bf ? run_stage<kBF16, true>(x, a.gate, a.gate_scale, a.up, a.up_scale, a.n, a.hidden,
@@ -320,24 +385,6 @@ hipError_t launch_stream_mlp(const MlpArgs& a, int stage, hipStream_t st) {
               : run_stage<kF16, false>(h, a.down, a.down_scale, nullptr, nullptr, a.n, a.inter, a.hidden, y, st);
   }
   return hipSuccess;
-}
-
-bool stream_supported(const MlpArgs& a, int stage) {
-  const DevCaps d = caps();
-  if (d.cus < 1 || a.n < 1 || a.n > 8) return false;
-  auto fits = [&](int64_t K, int mats) {
-    if (K % kItemK != 0) return false;
-    const int64_t items = mats * (K / kItemK);
-    if ((items + kNW - 1) / kNW > 8) return false;
-    const int64_t lds = a.n * (2 * K + 16) + 2 * (int64_t)kNW * mats * 64 * 4;
-    return lds <= d.max_lds;
-  };
-  if ((stage & kStageGateUp) && !fits(a.hidden, 2)) return false;
-  if ((stage & kStageDown) && !fits(a.inter, 1)) return false;
-  const void* ptrs[] = {a.x, a.gate, a.up, a.down, a.tmp};
-  for (const void* p : ptrs)
-    if (p && !aligned16(p)) return false;
-  return true;
 }
 
 }  // namespace tinyinfer
