@@ -5,31 +5,34 @@
 // 365-426): gate_up with the SiLU*up epilogue writes h, down writes out.
 //
 // Memory order is what decides HBM efficiency here, so the work is laid out
-// around the load stream (each choice measured on MI355X with load-only
-// probes of the same instruction shapes):
+// around the load stream (each choice measured on MI355X):
 //   * an item is 8 weight rows x 128 contiguous bytes (256 K elements): one
 //     dwordx4 load per lane, 8 full cache lines per instruction;
 //   * a row group is 8 rows x all of K (x both matrices for gate_up).
-//     Workgroup g takes row groups g, g+G, g+2G, ... and each of its waves a
-//     contiguous run of the row group's K segments, so the whole chip reads
-//     one contiguous band of each matrix at a time;
-//   * one 8-wave workgroup per CU, each wave with its next row group's loads
-//     in flight while it multiplies the current one (8 waves/CU streaming a
-//     few loads each gave the highest bandwidth; more waves gave less);
-//   * no workgroup barrier in the stream: a wave stores its partial sums in
-//     an LDS slot of the row group and bumps an LDS counter; the last wave to
-//     finish a row group sums the slots in a fixed order (bit-reproducible)
-//     and runs the epilogue;
-//   * a wave fetches the e8m0 scale bytes of its segments with one 8-byte load
-//     per (row, segment) ahead of its weights and stages them in its own LDS
-//     area (a scale-byte load per weight instruction costs ~20% bandwidth).
-// x is staged in LDS once per workgroup, after the first row groups' loads.
+//     Workgroup g takes row groups g, g+G, g+2G, ...; wave w of it takes a
+//     contiguous run of the row group's K segments (1/8 of K), so the whole
+//     chip reads one band of each matrix at a time;
+//   * a wave's share of a row group is cut into units of SPU segments; the
+//     wave keeps two units in flight (loads of unit u+2 are issued as soon as
+//     unit u has been multiplied);
+//   * one 8-wave workgroup per CU and no workgroup barrier in the stream: at
+//     the end of a row group a wave stores its partial sums in an LDS slot of
+//     the row group and bumps an LDS counter; the last wave to get there sums
+//     the slots in a fixed order (bit-reproducible) and runs the epilogue;
+//   * x and the e8m0 bytes of all of the workgroup's row groups are staged in
+//     LDS by a prologue, with whole-line loads issued before the first
+//     weights (loads complete in issue order, so anything issued after the
+//     weights would wait for them).  Scale bytes fetched per unit instead cost
+//     about as many cache-line requests as the weights themselves.
 //
 // MFMA mapping ("8 rows x 128 B"): lane l holds weight row l&7, 32-element K
 // block l>>3 of the item.  With these as the A operand of
 // v_mfma_f32_16x16x32_bf16, MFMA row i is weight row i&7 over K blocks
 // {2g + (i>>3)}; the B operand in lane l carries token (l%16)&7 at lane l's
 // own K block, so y[row r][token t] = C[r][t] + C[r+8][t+8] (r, t < 8).
+#include <cstdlib>
+#include <type_traits>
+
 #include "mxfp4_common.hpp"
 #include "mxfp4_launch.hpp"
 
@@ -39,8 +42,9 @@ namespace {
 
 constexpr int kNW = 8;            // waves per workgroup
 constexpr int kItemK = 256;       // K elements per item (one 128-byte segment per row)
-constexpr int kMaxSpw = 8;        // max segments per wave per matrix (more would spill)
-constexpr int kSclPerWave = 2 * 8 * kMaxSpw * 8;   // wave-private scale bytes (mats x rows x segs x 8)
+constexpr int kMaxSpw = 8;        // max K segments per wave per row group
+constexpr int kXPre = 4;          // x chunks per thread loaded ahead of the weights
+constexpr int kSPre = 4;          // scale chunks per thread loaded ahead of the weights
 
 struct StreamArgs {
   const uint16_t* x;      // [M, K] activations (x for gate_up, h for down)
@@ -51,10 +55,14 @@ struct StreamArgs {
   uint16_t* out;          // [M, R]
   int M, K, R;
   int segs;               // K / kItemK
+  int spu;                // segments per unit
+  int parts;              // units per row group per wave
   int rgroups;            // R / 8
   int nrg_max;            // max row groups per workgroup
-  int xs_stride;          // bytes per staged token row
-  int lds_scl, lds_red, lds_cnt;   // LDS byte offsets
+  int xs_stride;          // LDS bytes per staged token row
+  int ss_stride;          // LDS bytes per staged scale row (K/32 + 16: rows fall in different banks)
+  int xreg;               // activations in VGPRs (else staged in LDS)
+  int lds_scl, lds_red, lds_cnt, lds_out;   // LDS byte offsets
 };
 
 // Wave w's segment run [lo, hi) of a row group (same for both matrices).
@@ -63,112 +71,114 @@ __device__ __forceinline__ void seg_run(const StreamArgs& a, int wave, int& lo, 
   hi = a.segs * (wave + 1) / kNW;
 }
 
-// A row group's loads for this wave: scale bytes (8-byte pieces, one per
-// (matrix, row, segment), SPL per lane) first, then the weight items
-// (matrix-major, then segment).  A fixed instruction count: unused slots read
-// the matrices' first bytes and are not used.
-template <int SPW, bool GATEUP, int SPL>
-__device__ __forceinline__ void issue_rg(const StreamArgs& a, int rg, int wave,
-                                         u32x4_t (&wv)[(GATEUP ? 2 : 1) * SPW], u32x2_t (&sc)[SPL]) {
+// Segments [s0, s0 + nu) of the wave's run belong to unit `part`.
+__device__ __forceinline__ void unit_segs(const StreamArgs& a, int wave, int part, int spu, int& s0, int& nu) {
+  int lo, hi;
+  seg_run(a, wave, lo, hi);
+  s0 = lo + part * spu;
+  const int e = s0 + spu < hi ? s0 + spu : hi;
+  nu = e > s0 ? e - s0 : 0;
+}
+
+// A unit's weight items (matrix-major).  A fixed instruction count: a slot
+// outside the unit repeats the load of a segment the unit (or a neighbouring
+// wave) does read, and is not used.  Repeats of real addresses hit in cache;
+// a common dummy address instead would send every wave of the chip to one L2
+// channel.
+template <int SPU, bool GATEUP>
+__device__ __forceinline__ void issue_unit(const StreamArgs& a, int rg, int part, int wave,
+                                           u32x4_t (&wv)[(GATEUP ? 2 : 1) * SPU]) {
   constexpr int kMats = GATEUP ? 2 : 1;
   const int lane = threadIdx.x & 63;
   const int r8 = lane & 7, q8 = lane >> 3;
-  int lo, hi;
-  seg_run(a, wave, lo, hi);
-  const int n = hi - lo;
-  const int nn = n > 0 ? n : 1;
-  const bool rg_ok = rg < a.rgroups;
-  const int64_t rgc = rg_ok ? rg : 0;
-#pragma unroll
-  for (int i = 0; i < SPL; ++i) {
-    const int p = lane + 64 * i;                 // piece (mat, row, seg): p = (mat * 8 + row) * n + seg
-    const bool ok = rg_ok && p < kMats * 8 * n;
-    const int pc = ok ? p : 0;
-    const int mr = pc / nn, sg = pc - mr * nn;
-    const int mat = GATEUP ? mr / 8 : 0;
-    const int row = mr - mat * 8;
-    const uint8_t* s = mat ? a.s1 : a.s0;
-    const uint8_t* sp = ok ? s + (rgc * 8 + row) * (a.K / 32) + (int64_t)(lo + sg) * 8 : a.s0;
-    sc[i] = *reinterpret_cast<const u32x2_t*>(sp);
+  int s0, nu;
+  unit_segs(a, wave, part, SPU, s0, nu);
+  if (nu == 0) {                 // a wave with a shorter run: repeat its first segment
+    int hi;
+    seg_run(a, wave, s0, hi);
   }
-  const int64_t row = rgc * 8 + r8;
+  const int last = nu > 0 ? nu - 1 : 0;
+  const int64_t row = (int64_t)rg * 8 + r8;
 #pragma unroll
-  for (int k = 0; k < kMats * SPW; ++k) {
-    const int mat = GATEUP ? k / SPW : 0;
-    const int sg = k - mat * SPW;
-    const bool ok = rg_ok && sg < n;
+  for (int k = 0; k < kMats * SPU; ++k) {
+    const int mat = GATEUP ? k / SPU : 0;
+    const int sg = k - mat * SPU < last ? k - mat * SPU : last;
     const uint8_t* w = mat ? a.w1 : a.w0;
-    const uint8_t* wp = ok ? w + row * (a.K / 2) + (int64_t)(lo + sg) * (kItemK / 2) + 16 * q8 : a.w0;
+    const uint8_t* wp = w + row * (a.K / 2) + (int64_t)(s0 + sg) * (kItemK / 2) + 16 * q8;
     wv[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wp));
   }
+  // units complete in issue order only if they are issued in program order:
+  // keep the scheduler from interleaving two units' loads
+  __builtin_amdgcn_sched_barrier(0);
 }
 
-// Multiply this wave's items of one row group (FAST: every scale byte in the
+// Multiply one unit's items into acc (FAST: every scale byte in the
 // hardware-exact range; chosen once outside this body so each conversion
-// sits in the same basic block as its MFMA).
-template <int DT, int SPW, bool GATEUP, bool FAST>
-__device__ __forceinline__ void mma_items(int n, int lo, const u32x4_t (&wv)[(GATEUP ? 2 : 1) * SPW],
-                                          const uint32_t (&sb)[(GATEUP ? 2 : 1) * SPW], const uint8_t* xrow,
-                                          f32x4_t (&acc)[2]) {
+// sits in the same basic block as its MFMA).  Every item goes through the
+// MFMA: a branch around the slots outside the unit would leave some loads
+// unconsumed on one path, and the compiler then drains the whole load queue
+// (vmcnt(0)) before the next issue, which serialises the pipeline.  FULL
+// units (all slots inside, the common case) take no masking: a wave64 select
+// costs as much as one of the four conversions an MFMA needs.  Otherwise the
+// outside slots multiply zero weights by zero activations.
+// xf(sg, t) returns the activation operand of segment sg of the unit, MFMA t.
+template <int DT, int SPU, bool GATEUP, bool FAST, bool FULL, typename XF>
+__device__ __forceinline__ void mma_unit(int nu, const u32x4_t (&wv)[(GATEUP ? 2 : 1) * SPU],
+                                         const uint32_t (&sb)[(GATEUP ? 2 : 1) * SPU], const XF& xf,
+                                         f32x4_t (&acc)[2]) {
   constexpr int kMats = GATEUP ? 2 : 1;
-  const int q8 = (threadIdx.x & 63) >> 3;
 #pragma unroll
   for (int mat = 0; mat < kMats; ++mat) {
 #pragma unroll
-    for (int sg = 0; sg < SPW; ++sg) {
-      if (sg >= n) break;                                   // wave-uniform
-      const int k = mat * SPW + sg;
-      const int kx = (lo + sg) * kItemK + 32 * q8;
+    for (int sg = 0; sg < SPU; ++sg) {
+      const int k = mat * SPU + sg;
+      const bool live = FULL || sg < nu;                    // wave-uniform
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const u32x4_t wa = FAST ? dq8_bf16_fast(wv[k][t], sb[k]) : dq8_bf16_exact(wv[k][t], sb[k]);
-        const u32x4_t xb = *reinterpret_cast<const u32x4_t*>(xrow + 2 * (kx + 8 * t));
+        const uint32_t wq = live ? wv[k][t] : 0u;           // e2m1 code 0 is +0
+        const u32x4_t wa = FAST ? dq8_bf16_fast(wq, sb[k]) : dq8_bf16_exact(wq, sb[k]);
+        const u32x4_t xr = xf(live ? sg : 0, t);
+        const u32x4_t xb = live ? xr : u32x4_t{0u, 0u, 0u, 0u};   // 0 * (inf or nan in x) stays out
         if constexpr (DT == kBF16) {
           acc[mat] = mfma16x16x32(wa, xb, acc[mat]);
         } else {
-          u32x4_t xh, xl;
-          f16x8_split_bf16(xb, xh, xl);
-          acc[mat] = mfma16x16x32(wa, xl, mfma16x16x32(wa, xh, acc[mat]));
+          u32x4_t xh, xlo;
+          f16x8_split_bf16(xb, xh, xlo);
+          acc[mat] = mfma16x16x32(wa, xlo, mfma16x16x32(wa, xh, acc[mat]));
         }
       }
     }
   }
 }
 
-template <int DT, int SPW, bool GATEUP, int SPL>
-__device__ __forceinline__ void compute_rg(const StreamArgs& a, int wave,
-                                           const u32x4_t (&wv)[(GATEUP ? 2 : 1) * SPW],
-                                           const u32x2_t (&sc)[SPL], uint8_t* my_scl, const uint8_t* xs,
-                                           f32x4_t (&acc)[2]) {
+// Scale bytes of unit `part` of the workgroup's li-th row group, from the
+// LDS copy ([li][mat][row] rows of ss_stride bytes), then the multiply.
+// The activations come from xf(segment of the unit, t).
+template <int DT, int SPU, bool GATEUP, typename XF>
+__device__ __forceinline__ void compute_unit(const StreamArgs& a, int wave, int li, int part,
+                                             const u32x4_t (&wv)[(GATEUP ? 2 : 1) * SPU], const uint8_t* scl,
+                                             const XF& xf, f32x4_t (&acc)[2]) {
   constexpr int kMats = GATEUP ? 2 : 1;
   const int lane = threadIdx.x & 63;
   const int r8 = lane & 7, q8 = lane >> 3;
-  int lo, hi;
-  seg_run(a, wave, lo, hi);
-  const int n = hi - lo;
-  // stage this wave's scale pieces ([mat][row][seg] x 8 bytes) and read back
-  // the byte of each of this lane's items
-#pragma unroll
-  for (int i = 0; i < SPL; ++i) {
-    const int p = lane + 64 * i;
-    if (p < kMats * 8 * n) *reinterpret_cast<u32x2_t*>(my_scl + 8 * p) = sc[i];
-  }
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");   // other lanes' bytes are read back
-  uint32_t sb[kMats * SPW];
+  int s0, nu;
+  unit_segs(a, wave, part, SPU, s0, nu);
+  uint32_t sb[kMats * SPU];
   bool ok = true;
 #pragma unroll
-  for (int k = 0; k < kMats * SPW; ++k) {
-    const int mat = GATEUP ? k / SPW : 0;
-    const int sg = k - mat * SPW;
-    sb[k] = sg < n ? (uint32_t)my_scl[8 * ((mat * 8 + r8) * n + sg) + q8] : 127u;
+  for (int k = 0; k < kMats * SPU; ++k) {
+    const int mat = GATEUP ? k / SPU : 0;
+    const int sg = k - mat * SPU;
+    const uint8_t* srow = scl + ((li * kMats + mat) * 8 + r8) * a.ss_stride;
+    sb[k] = sg < nu ? (uint32_t)srow[(s0 + sg) * 8 + q8] : 127u;
     ok = ok && e8m0_fast_ok(sb[k]);
   }
-  const int c = lane & 15;
-  const int tok = (c & 7) < a.M ? (c & 7) : a.M - 1;     // columns >= M are discarded
-  const uint8_t* xrow = xs + tok * a.xs_stride;
-  acc[0] = acc[1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  if (wave_all(ok)) mma_items<DT, SPW, GATEUP, true>(n, lo, wv, sb, xrow, acc);
-  else mma_items<DT, SPW, GATEUP, false>(n, lo, wv, sb, xrow, acc);
+  if (wave_all(ok)) {
+    if (nu == SPU) mma_unit<DT, SPU, GATEUP, true, true>(nu, wv, sb, xf, acc);
+    else mma_unit<DT, SPU, GATEUP, true, false>(nu, wv, sb, xf, acc);
+  } else {
+    mma_unit<DT, SPU, GATEUP, false, false>(nu, wv, sb, xf, acc);
+  }
 }
 
 // Fold C[r][t] + C[r+8][t+8] and store this wave's partial (rows 4g..4g+3,
@@ -182,54 +192,143 @@ __device__ __forceinline__ void store_partial(const f32x4_t& acc, float* red, in
   if (c < 8 && g < 2 && c < M) *reinterpret_cast<f32x4_t*>(red + c * 8 + 4 * g) = part;
 }
 
-template <int DT, int SPW, bool GATEUP, int SPL>
+// XREG: the wave's activations (its K range of every token, up to PMAX
+// units' worth) are copied from LDS into VGPRs once: a wave's K range is the
+// same in every row group, and reading them from LDS for every MFMA moves
+// twice the bytes the MFMAs consume (64 lanes x 16 B per instruction, 8 waves
+// sharing one LDS), which made gate_up's multiply LDS-bound.  The down stage
+// (longer K range per wave, more registers) measured faster reading LDS.
+// D units in flight per wave: 2 measured best (3 was slower everywhere).
+template <int DT, int SPU, bool GATEUP, int D, bool XREG, int PMAX>
 __global__ __launch_bounds__(kNW * 64, 1) void stream_kernel(StreamArgs a) {
+  static_assert(D == 2 || D == 3, "units in flight per wave");
+  static_assert(PMAX == 1 || PMAX == 2, "units per row group with activations in registers");
+  static_assert(!XREG || DT == kBF16, "fp16 activations are split into two bf16 operands in LDS");
   constexpr int kMats = GATEUP ? 2 : 1;
-  constexpr int kItems = kMats * SPW;
+  constexpr int kItems = kMats * SPU;
+  constexpr int kThreads = kNW * 64;
+  constexpr int kNX = XREG ? PMAX * SPU : 1;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int G = gridDim.x;
   const int g = blockIdx.x;
-  uint8_t* my_scl = lds + a.lds_scl + wave * kSclPerWave;
+  uint8_t* scl = lds + a.lds_scl;                                           // [nrg_max][kMats][8][ss_stride]
   float* red = reinterpret_cast<float*>(lds + a.lds_red);                   // [nrg_max][kNW][kMats][64]
   unsigned int* cnt = reinterpret_cast<unsigned int*>(lds + a.lds_cnt);    // [nrg_max]
+  uint16_t* outs = reinterpret_cast<uint16_t*>(lds + a.lds_out);           // [nrg_max][M][8]
+  const int P = a.parts;
+  const int nrg = (a.rgroups - g + G - 1) / G;
+  const int units = nrg * P;
+  const int q8 = lane >> 3;
+  const int tok = ((lane & 15) & 7) < a.M ? ((lane & 15) & 7) : a.M - 1;   // MFMA columns >= M are discarded
+  int lo, hi;
+  seg_run(a, wave, lo, hi);
 
-  u32x4_t wa[kItems], wb[kItems];
-  u32x2_t sca[SPL], scb[SPL];
-  issue_rg<SPW, GATEUP, SPL>(a, g, wave, wa, sca);
-  issue_rg<SPW, GATEUP, SPL>(a, g + G, wave, wb, scb);
+  for (int i = threadIdx.x; i < a.nrg_max; i += kThreads) cnt[i] = 0u;
 
-  // stage x [M, K] and clear the row-group counters
-  {
-    constexpr int kB = 4;
-    const int per_row = a.K / 8;
-    const int n = a.M * per_row;
-    for (int c0 = threadIdx.x; c0 < n; c0 += kB * kNW * 64) {
-      u32x4_t v[kB];
+  // Prologue: x and the scale bytes of all of this workgroup's row groups go
+  // to LDS, loaded before the first weights (loads complete in issue order,
+  // so anything issued after the weights would wait for them).
+  // LDS x chunk c (16 bytes): token c / (K/8), elements 8 (c % (K/8)).
+  const int x_row = a.K / 8;
+  const int nxc = a.M * x_row;
+  auto x_src = [&](int c) {
+    const int cc = c < nxc ? c : nxc - 1;
+    const int t = cc / x_row, k8 = cc - t * x_row;
+    return reinterpret_cast<const u32x4_t*>(a.x + (int64_t)t * a.K + 8 * k8);
+  };
+  auto x_dst = [&](int c) {
+    const int t = c / x_row, k8 = c - t * x_row;
+    return reinterpret_cast<u32x4_t*>(lds + t * a.xs_stride + 16 * k8);
+  };
+  // scale chunk c (16 bytes): block (li, mat) = c / (K/64), which is rows
+  // rg*8 .. rg*8+7 of that matrix's scales, contiguous in memory
+  const int s_blk = a.K / 64;
+  const int nsc = nrg * kMats * s_blk;
+  auto s_src = [&](int c) {
+    const int cc = c < nsc ? c : nsc - 1;
+    const int blk = cc / s_blk, off = 16 * (cc - blk * s_blk);
+    const int li = blk / kMats, mat = blk - li * kMats;
+    const uint8_t* sp = mat ? a.s1 : a.s0;
+    return reinterpret_cast<const u32x4_t*>(sp + (int64_t)(g + li * G) * 8 * (a.K / 32) + off);
+  };
+  auto s_dst = [&](int c) {
+    const int blk = c / s_blk, off = 16 * (c - blk * s_blk);
+    const int row = off / (a.K / 32), col = off - row * (a.K / 32);
+    return reinterpret_cast<u32x4_t*>(scl + (blk * 8 + row) * a.ss_stride + col);
+  };
+  // chunks beyond the per-thread preload (large M, many row groups per
+  // workgroup): these wait for their own loads, before any weight is issued
+  for (int c0 = threadIdx.x + kXPre * kThreads; c0 < nxc; c0 += 4 * kThreads) {
+    u32x4_t v[4];
 #pragma unroll
-      for (int b = 0; b < kB; ++b) {
-        const int cidx = c0 + b * kNW * 64;
-        const int cc = cidx < n ? cidx : n - 1;
-        const int t = cc / per_row, k8 = cc - t * per_row;
-        v[b] = *reinterpret_cast<const u32x4_t*>(a.x + (int64_t)t * a.K + 8 * k8);
-      }
+    for (int b = 0; b < 4; ++b) v[b] = *x_src(c0 + b * kThreads);
 #pragma unroll
-      for (int b = 0; b < kB; ++b) {
-        const int cidx = c0 + b * kNW * 64;
-        if (cidx < n) {
-          const int t = cidx / per_row, k8 = cidx - t * per_row;
-          *reinterpret_cast<u32x4_t*>(lds + t * a.xs_stride + 16 * k8) = v[b];
-        }
-      }
-    }
-    for (int i = threadIdx.x; i < a.nrg_max; i += kNW * 64) cnt[i] = 0u;
+    for (int b = 0; b < 4; ++b)
+      if (c0 + b * kThreads < nxc) *x_dst(c0 + b * kThreads) = v[b];
   }
-  __syncthreads();
+  for (int c0 = threadIdx.x + kSPre * kThreads; c0 < nsc; c0 += 4 * kThreads) {
+    u32x4_t v[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) v[b] = *s_src(c0 + b * kThreads);
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      if (c0 + b * kThreads < nsc) *s_dst(c0 + b * kThreads) = v[b];
+  }
+  u32x4_t xv[kXPre], sv[kSPre];
+#pragma unroll
+  for (int b = 0; b < kXPre; ++b) xv[b] = *x_src(threadIdx.x + b * kThreads);
+#pragma unroll
+  for (int b = 0; b < kSPre; ++b) sv[b] = *s_src(threadIdx.x + b * kThreads);
+
+  // the first D units in flight (separate named buffers: an array indexed by
+  // the pipeline slot ends up in scratch)
+  struct Buf {
+    u32x4_t w[kItems];
+  };
+  Buf b0, b1, b2;
+  auto issue = [&](Buf& b, int u) {
+    const int uu = u < units ? u : units - 1;    // past the end: repeat the last unit's loads
+    const int rgi = uu / P, part = uu - rgi * P;
+    issue_unit<SPU, GATEUP>(a, g + rgi * G, part, wave, b.w);
+  };
+  issue(b0, 0);
+  issue(b1, 1);
+  if constexpr (D > 2) issue(b2, 2);
+
+#pragma unroll
+  for (int b = 0; b < kXPre; ++b)
+    if (threadIdx.x + b * kThreads < nxc) *x_dst(threadIdx.x + b * kThreads) = xv[b];
+#pragma unroll
+  for (int b = 0; b < kSPre; ++b)
+    if (threadIdx.x + b * kThreads < nsc) *s_dst(threadIdx.x + b * kThreads) = sv[b];
+  // every wave's LDS stores (counters, x, scales) are done before any wave
+  // reads them: wait for LDS only (a full __syncthreads would also wait for
+  // the weights in flight)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);    // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+
+  // XREG: segment j of the wave's run, MFMA t: x[tok][256 (lo + j) + 32 q8 + 8 t],
+  // copied once from LDS; segments past the run read a valid address and are
+  // never used unmasked.
+  const uint8_t* xrow = lds + tok * a.xs_stride;
+  u32x4_t xr[kNX][4];
+  if constexpr (XREG) {
+#pragma unroll
+    for (int j = 0; j < kNX; ++j) {
+      const int seg = lo + j < a.segs ? lo + j : a.segs - 1;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        xr[j][t] = *reinterpret_cast<const u32x4_t*>(xrow + 2 * (seg * kItemK + 32 * q8 + 8 * t));
+    }
+  }
 
   // after a row group: partials into its slot, count, and the last wave of
-  // the workgroup to get here runs the epilogue
-  auto finish_rg = [&](int rg, int li, const f32x4_t (&acc)[2]) {
+  // the workgroup to get here runs the epilogue into LDS
+  auto finish_rg = [&](int li, const f32x4_t (&acc)[2]) {
     float* slot = red + (int64_t)li * (kNW * kMats * 64);
 #pragma unroll
     for (int m = 0; m < kMats; ++m) store_partial(acc[m], slot + (wave * kMats + m) * 64, a.M);
@@ -248,21 +347,63 @@ __global__ __launch_bounds__(kNW * 64, 1) void stream_kernel(StreamArgs a) {
           if (GATEUP) y1 += slot[(w * kMats + 1) * 64 + t * 8 + r];
         }
         const float v = GATEUP ? silu_f32(y0) * y1 : y0;
-        a.out[(int64_t)t * a.R + rg * 8 + r] = f32_to_act<DT>(v);
+        outs[(li * a.M + t) * 8 + r] = f32_to_act<DT>(v);
       }
     }
   };
 
-  int li = 0;
-  for (int rg = g; rg < a.rgroups; rg += 2 * G, li += 2) {
-    f32x4_t acc[2];
-    compute_rg<DT, SPW, GATEUP, SPL>(a, wave, wa, sca, my_scl, lds, acc);
-    issue_rg<SPW, GATEUP, SPL>(a, rg + 2 * G, wave, wa, sca);
-    finish_rg(rg, li, acc);
-    if (rg + G >= a.rgroups) break;
-    compute_rg<DT, SPW, GATEUP, SPL>(a, wave, wb, scb, my_scl, lds, acc);
-    issue_rg<SPW, GATEUP, SPL>(a, rg + 3 * G, wave, wb, scb);
-    finish_rg(rg + G, li + 1, acc);
+  // unit u = (row group g + (u / P) G, part u % P) uses buffer u % D
+  f32x4_t acc[2];
+  auto compute = [&](Buf& b, int rgi, int part) {
+    if constexpr (XREG) {
+      // part selects which of the wave's segments: a compile-time index into
+      // the activation registers
+      auto run = [&](auto part_tag) {
+        constexpr int PT = decltype(part_tag)::value;
+        auto xf = [&](int sg, int t) { return xr[PT * SPU + sg][t]; };
+        compute_unit<DT, SPU, GATEUP>(a, wave, rgi, PT, b.w, scl, xf, acc);
+      };
+      if (PMAX == 1 || part == 0) run(std::integral_constant<int, 0>{});
+      else run(std::integral_constant<int, PMAX - 1>{});
+    } else {
+      auto xf = [&](int sg, int t) {
+        int s0, nu;
+        unit_segs(a, wave, part, SPU, s0, nu);
+        return *reinterpret_cast<const u32x4_t*>(xrow + 2 * ((s0 + sg) * kItemK + 32 * q8 + 8 * t));
+      };
+      compute_unit<DT, SPU, GATEUP>(a, wave, rgi, part, b.w, scl, xf, acc);
+    }
+  };
+  auto step = [&](Buf& b, int u) {
+    const int rgi = u / P, part = u - rgi * P;
+    if (part == 0) acc[0] = acc[1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    compute(b, rgi, part);
+    issue(b, u + D);
+    if (part == P - 1) finish_rg(rgi, acc);
+  };
+  // One exit, at the top: a break between the steps would join the loop's
+  // back edge with a path on which the buffers were issued in another order,
+  // and the compiler's load-queue bookkeeping would then wait for all of them
+  // at the top of every iteration.
+  int u = 0;
+  for (; u + D - 1 < units; u += D) {
+    step(b0, u);
+    step(b1, u + 1);
+    if constexpr (D > 2) step(b2, u + 2);
+  }
+  if (u < units) step(b0, u);
+  if constexpr (D > 2) {
+    if (u + 1 < units) step(b1, u + 1);
+  }
+
+  // the row groups' outputs, staged in LDS by their last waves (a global
+  // store inside the stream would make the load-queue accounting
+  // path-dependent, see mma_unit)
+  __syncthreads();
+  for (int i = threadIdx.x; i < nrg * a.M * 8; i += kThreads) {
+    const int li = i / (a.M * 8), rem = i - li * a.M * 8;
+    const int t = rem >> 3, r = rem & 7;
+    a.out[(int64_t)t * a.R + (int64_t)(g + li * G) * 8 + r] = outs[i];
   }
 }
 
@@ -291,10 +432,38 @@ DevCaps caps() {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+int env_int(const char* name, int dflt, int lo, int hi) {
+  const char* e = std::getenv(name);
+  const int v = e ? std::atoi(e) : dflt;
+  return v < lo ? lo : (v > hi ? hi : v);
+}
+
+// Segments per unit for a wave run of up to `spw` segments: the fewest units
+// with at most 4 weight items each (gate_up reads two matrices per segment),
+// spread evenly.  TINYINFER_STREAM_SPU_GU / _DN override it for tuning.
+int stream_spu(bool gateup, int spw) {
+  static const int gu = env_int("TINYINFER_STREAM_SPU_GU", 0, 0, 2);
+  static const int dn = env_int("TINYINFER_STREAM_SPU_DN", 0, 0, 4);
+  const int forced = gateup ? gu : dn;
+  if (forced > 0) return forced;
+  const int cap = gateup ? 2 : 4;
+  const int parts = (spw + cap - 1) / cap;
+  return (spw + parts - 1) / parts;
+}
+
+constexpr int kDepth = 2;         // units in flight per wave
+
+// Activations in registers for gate_up (TINYINFER_STREAM_XREG=0 turns it off).
+bool stream_xreg_allowed(bool gateup) {
+  static const int v = env_int("TINYINFER_STREAM_XREG", 1, 0, 1);
+  return v == 1 && gateup;
+}
+
 // Geometry of one stage; false when the streaming kernel does not apply.
-bool plan(int64_t M, int64_t K, int64_t R, bool gateup, const DevCaps& d, StreamArgs& a, int& grid,
+bool plan(int64_t M, int64_t K, int64_t R, bool gateup, bool bf16, const DevCaps& d, StreamArgs& a, int& grid,
           int64_t& lds) {
-  if (d.cus < 1 || M < 1 || M > 8 || K % kItemK != 0 || R % 8 != 0) return false;
+  // K % 512: a row group's scale rows split into whole 16-byte chunks
+  if (d.cus < 1 || M < 1 || M > 8 || K % (2 * kItemK) != 0 || R % 8 != 0) return false;
   if (K > (1 << 20) || R > (1 << 24)) return false;
   const int mats = gateup ? 2 : 1;
   a.M = (int)M;
@@ -302,22 +471,26 @@ bool plan(int64_t M, int64_t K, int64_t R, bool gateup, const DevCaps& d, Stream
   a.R = (int)R;
   a.segs = (int)(K / kItemK);
   const int spw = (a.segs + kNW - 1) / kNW;
-  if (spw > (gateup ? kMaxSpw / 2 : kMaxSpw)) return false;   // double-buffered items fit in VGPRs
-  if (mats * 8 * spw > 64) return false;             // scale pieces: one per lane
+  if (spw > kMaxSpw) return false;
+  a.spu = stream_spu(gateup, spw);
+  a.parts = (spw + a.spu - 1) / a.spu;
   a.rgroups = (int)(R / 8);
   grid = d.cus < a.rgroups ? d.cus : a.rgroups;
   a.nrg_max = (a.rgroups + grid - 1) / grid;
   a.xs_stride = (int)(2 * K + 16);
+  a.ss_stride = (int)(K / 32 + 16);
+  // register budget (2 waves per SIMD, 256 VGPRs each): one unit's activations
+  a.xreg = bf16 && stream_xreg_allowed(gateup) && a.parts == 1;
   a.lds_scl = (int)(M * a.xs_stride);
-  a.lds_red = a.lds_scl + kNW * kSclPerWave;
+  a.lds_red = a.lds_scl + a.nrg_max * mats * 8 * a.ss_stride;
   a.lds_cnt = a.lds_red + a.nrg_max * kNW * mats * 64 * 4;
-  lds = a.lds_cnt + 4 * ((a.nrg_max + 3) & ~3);
+  a.lds_out = a.lds_cnt + 4 * ((a.nrg_max + 3) & ~3);
+  lds = a.lds_out + a.nrg_max * (int)M * 8 * 2;
   return lds <= d.max_lds;
 }
 
 template <int DT, bool GATEUP>
 hipError_t launch(const StreamArgs& a, int64_t lds, int grid, hipStream_t st) {
-  const int spw = (a.segs + kNW - 1) / kNW;
   auto go = [&](auto kern) -> hipError_t {
     if (lds > 64 * 1024 &&
         hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -328,9 +501,21 @@ hipError_t launch(const StreamArgs& a, int64_t lds, int grid, hipStream_t st) {
     kern<<<grid, kNW * 64, (size_t)lds, st>>>(a);
     return hipGetLastError();
   };
-  if (spw <= 2) return go(stream_kernel<DT, 2, GATEUP, 1>);
-  if (GATEUP || spw <= 4) return go(stream_kernel<DT, 4, GATEUP, 1>);
-  return go(stream_kernel<DT, 8, false, 1>);
+  auto depth = [&](auto spu_tag) -> hipError_t {
+    constexpr int S = decltype(spu_tag)::value;
+    if constexpr (DT == kBF16 && GATEUP) {
+      if (a.xreg) return go(stream_kernel<DT, S, GATEUP, kDepth, true, 1>);
+    }
+    return go(stream_kernel<DT, S, GATEUP, kDepth, false, 1>);
+  };
+  if (a.spu <= 1) return depth(std::integral_constant<int, 1>{});
+  if constexpr (GATEUP) {
+    return depth(std::integral_constant<int, 2>{});
+  } else {
+    if (a.spu == 2) return depth(std::integral_constant<int, 2>{});
+    if (a.spu == 3) return depth(std::integral_constant<int, 3>{});
+    return depth(std::integral_constant<int, 4>{});
+  }
 }
 
 template <int DT, bool GATEUP>
@@ -339,7 +524,7 @@ hipError_t run_stage(const uint16_t* x, const uint8_t* w0, const uint8_t* s0, co
   StreamArgs a;
   int grid = 0;
   int64_t lds = 0;
-  if (!plan(M, K, R, GATEUP, caps(), a, grid, lds)) return hipErrorNotSupported;
+  if (!plan(M, K, R, GATEUP, DT == kBF16, caps(), a, grid, lds)) return hipErrorNotSupported;
   a.x = x;
   a.w0 = w0;
   a.s0 = s0;
@@ -356,15 +541,13 @@ bool stream_supported(const MlpArgs& a, int stage) {
   StreamArgs sa;
   int grid = 0;
   int64_t lds = 0;
-  if ((stage & kStageGateUp) && !plan(a.n, a.hidden, a.inter, true, d, sa, grid, lds)) return false;
-  if ((stage & kStageDown) && !plan(a.n, a.inter, a.hidden, false, d, sa, grid, lds)) return false;
-  // 16-byte loads of activations and weights, 8-byte loads of scale bytes
-  const void* p16[] = {a.x, a.gate, a.up, a.down, a.tmp};
+  const bool bf = a.dtype == kBF16;
+  if ((stage & kStageGateUp) && !plan(a.n, a.hidden, a.inter, true, bf, d, sa, grid, lds)) return false;
+  if ((stage & kStageDown) && !plan(a.n, a.inter, a.hidden, false, bf, d, sa, grid, lds)) return false;
+  // 16-byte loads of activations, weights and scale rows
+  const void* p16[] = {a.x, a.gate, a.up, a.down, a.tmp, a.gate_scale, a.up_scale, a.down_scale};
   for (const void* p : p16)
     if (p && !aligned16(p)) return false;
-  const void* p8[] = {a.gate_scale, a.up_scale, a.down_scale};
-  for (const void* p : p8)
-    if (p && (reinterpret_cast<uintptr_t>(p) & 7u)) return false;
   return true;
 }
 
