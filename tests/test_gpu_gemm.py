@@ -1,0 +1,99 @@
+"""GPU parity of the prefill GEMM path (TI_PATH_GEMM, and TI_PATH_AUTO at
+N >= 96): the direct-to-LDS ring kernels for bf16 activations with hidden and
+intermediate multiples of 512, the register-staged GEMM otherwise.
+
+Each stage is called through its C-ABI entry point and compared with the CPU
+oracle at the kernel's rounding points (exact sums, h rounded once to the
+activation dtype): a few bf16 ulps. Cases: partial token tiles, the Qwen3
+block shapes, scale bytes outside the hardware conversion's exact range,
+fp16 activations (register-staged kernel), bit-reproducibility."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import mlp as om
+from tests.helpers import banner, make_case, to_dev
+from tests.test_gpu_stream import check_close, down_semantics, h_semantics
+
+pytestmark = pytest.mark.gpu
+
+GEMM = 2
+
+
+@pytest.fixture(scope="module")
+def capi():
+    from tinyinfer_amd import capi as c
+    return c
+
+
+def run_gemm_stages(capi, x, mats, what, cols=None):
+    xd, md = to_dev(x, mats)
+    gp, gs, up, us, dp, ds = mats
+    h = capi.gate_up(xd, *md[:4], path=GEMM)
+    torch.cuda.synchronize()
+    h_ref = h_semantics(x, gp, gs, up, us)
+    check_close(h.cpu(), h_ref, f"{what} gate_up")
+    out = capi.down(h_ref.to("cuda"), md[4], md[5], path=GEMM)
+    torch.cuda.synchronize()
+    out, out_ref = out.cpu(), down_semantics(h_ref, dp, ds)
+    if cols is not None:
+        out, out_ref = out[:, cols], out_ref[:, cols]
+    check_close(out, out_ref, f"{what} down")
+    return out, out_ref
+
+
+@pytest.mark.parametrize("m", [96, 130, 256, 300, 513])
+def test_gemm_partial_token_tiles(capi, m):
+    banner(f"gemm m={m} h=1024 i=1536")
+    x, mats = make_case(m, 1024, 1536, seed=1000 + m)
+    run_gemm_stages(capi, x, mats, f"m={m}")
+
+
+@pytest.mark.parametrize("h,i,m", [(1024, 3072, 128), (2048, 6144, 200), (4096, 12288, 256)])
+def test_gemm_qwen3_shapes(capi, h, i, m):
+    """Qwen3-0.6B, 1.7B and 8B MLP shapes."""
+    banner(f"gemm qwen3 h={h} i={i} m={m}")
+    x, mats = make_case(m, h, i, seed=h + m)
+    run_gemm_stages(capi, x, mats, f"h={h} i={i} m={m}")
+
+
+def test_gemm_scale_bytes_outside_fast_range(capi):
+    """Scale bytes 0, 1, 253 and 254 take the exact dequantisation of a K step;
+    other steps of the same tiles stay on the hardware conversion."""
+    banner("gemm exact-scale branch")
+    x, mats = make_case(160, 1024, 2048, seed=91)
+    gp, gs, up, us, dp, ds = [np.array(a) for a in mats]
+    gs[3, 0] = 0
+    gs[700, 5] = 1
+    us[11, 31] = 1
+    for row, blk, byte in ((17, 9, 253), (900, 60, 254)):
+        ds[row, blk] = byte
+        dp[row, blk * 16:(blk + 1) * 16] = 0
+        dp[row, blk * 16 + 3] = 0x10
+    mats = [gp, gs, up, us, dp, ds]
+    big = [17, 900]
+    _, ref = run_gemm_stages(capi, x, mats, "exact-scale big rows", cols=big)
+    assert torch.isfinite(ref.float()).all() and ref.float().abs().min() > 1e30
+    run_gemm_stages(capi, x, mats, "exact-scale other rows", cols=[c for c in range(1024) if c not in big])
+
+
+def test_gemm_fp16_activations(capi):
+    banner("gemm fp16")
+    x, mats = make_case(130, 1024, 1536, seed=5, dtype=torch.float16)
+    run_gemm_stages(capi, x, mats, "fp16")
+
+
+def test_gemm_deterministic_and_full_call(capi):
+    """Two calls give the same bits; the full entry point equals its stages."""
+    banner("gemm determinism")
+    x, mats = make_case(300, 2048, 6144, seed=8)
+    xd, md = to_dev(x, mats)
+    a = capi.mlp_forward(xd, *md, path=GEMM)
+    b = capi.mlp_forward(xd, *md, path=GEMM)
+    tmp = capi.gate_up(xd, *md[:4], path=GEMM)
+    c = capi.down(tmp, *md[4:], path=GEMM)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert torch.equal(a.view(torch.int16), c.view(torch.int16))
+    check_close(a.cpu(), om.mlp_kernel_semantics(x, *mats), "1.7B m=300 full")

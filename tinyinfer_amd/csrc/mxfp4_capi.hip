@@ -85,7 +85,10 @@ int mlp_impl(const MlpArgs& a, int stage, int path, void* stream) {
     return to_status(e);
   }
   if (path == TI_PATH_AUTO) path = ((size_t)a.n >= kGemmMinTokens) ? TI_PATH_GEMM : TI_PATH_SKINNY;
-  if (path == TI_PATH_GEMM) return to_status(tinyinfer::launch_gemm_mlp(a, stage, s));
+  if (path == TI_PATH_GEMM) {
+    if (tinyinfer::gemm_ring_supported(a, stage)) return to_status(tinyinfer::launch_gemm_ring_mlp(a, stage, s));
+    return to_status(tinyinfer::launch_gemm_mlp(a, stage, s));
+  }
   // small batches: the streaming kernels where they apply (n <= 8), else the
   // 16-token-tile skinny kernels
   if ((size_t)a.n <= kStreamMaxTokens && tinyinfer::stream_supported(a, stage))

@@ -1,0 +1,324 @@
+// Tiled MXFP4 MLP GEMM for prefill (bf16 activations, K a multiple of 512):
+// a three-stage LDS ring fed by direct-to-LDS loads.
+//
+// Replaces the reference's per-token GEMV kernels mlp_stage1_mxfp4 /
+// mlp_stage2_mxfp4 (tinyinfer/csrc/mlp_fp4.cu:79-142, 365-426) where they are
+// compute-bound.  C = W X^T (weight rows x tokens) on v_mfma_f32_32x32x16_bf16
+// with fp32 accumulation; the e2m1 weights are dequantized to bf16 in
+// registers right before the MFMAs that use them.
+//
+// Workgroup: 512 threads (8 waves, 4 row groups x 2 token halves), one per
+// CU; a tile is 256 weight rows x BM tokens (gate_up: 128 output rows of gate
+// and of up, so the SiLU(g)*u epilogue has both in the same lanes; down: 256
+// output rows).  Per K step of 64:
+//   X  [BM tokens][64] bf16 = 128 B per token row,
+//   W  [256 rows][32 B packed],
+// loaded with global_load_lds_dwordx4 (each instruction writes 64 x 16 B
+// contiguously in LDS), so no VGPRs hold loads in flight and two stages can
+// be in flight while the third is multiplied.  Rows are XOR-swizzled in
+// 16-byte units on the global side (the LDS side of the load is fixed), so
+// that the MFMA operand reads (32 rows at one K offset) fall in distinct
+// banks: X chunk c of token row t sits at slot c ^ ((t >> 1) & 7), W half h of
+// row r at slot h ^ ((r >> 3) & 1).
+// The e8m0 bytes come 16 per row (8 K steps) with one extra load per wave
+// every 8 steps, double-buffered in LDS.
+//
+// Pipeline: stage k+2 is issued right after the barrier of step k (which
+// also proves stage k-1's buffer free), and each wave waits for its own
+// loads of stage k before that barrier with an explicit vmcnt.  The barrier
+// is a bare s_barrier: a __syncthreads fence would wait for every load in
+// flight, which the ring exists to avoid.
+//
+// Operand K order: in MFMA k-step s (0..3), lane half j (lane / 32) supplies
+// the 8 K elements 32j + 8s .. 32j + 8s + 7 of the step, for W and X alike
+// (a permutation of K shared by both operands leaves each dot product
+// unchanged).  A lane's W bytes for the step are then one 16-byte run under
+// one scale byte, and its X bytes one 64-byte run.
+#include <type_traits>
+
+#include "mxfp4_common.hpp"
+#include "mxfp4_launch.hpp"
+
+namespace tinyinfer {
+
+namespace {
+
+typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
+
+constexpr int kBK = 64;           // K per step
+constexpr int kNW = 8;            // waves
+constexpr int kThreads = kNW * 64;
+constexpr int kWRows = 256;       // weight rows per tile
+constexpr int kWBytes = kWRows * 32;      // packed W per stage
+constexpr int kSBlock = kWRows * 16;      // scale bytes per 8-step block
+constexpr int kStages = 3;
+
+template <int BM>
+struct RingCfg {
+  static constexpr int kXBytes = BM * 2 * kBK;                 // X per stage
+  static constexpr int kStage = kXBytes + kWBytes;
+  static constexpr int kLds = kStages * kStage + 2 * kSBlock;
+  static constexpr int kXInst = BM / 8 / kNW;                  // X loads per wave per stage
+  static constexpr int kTT = BM / 64;                          // 32-token blocks per wave
+  static_assert(kXInst >= 1 && kXInst * 8 * kNW == BM, "token tile must split over the waves");
+};
+
+struct RingArgs {
+  const uint16_t* x;        // [M, K]
+  const uint8_t* w[2];      // [N, K/2] (gate, up) or (down, down)
+  const uint8_t* s[2];      // [N, K/32]
+  uint16_t* out;            // [M, N]
+  int M, N, K;              // N: output rows
+  int m_tiles, n_tiles;
+};
+
+// 64 lanes x 16 bytes from per-lane global addresses to 1 KB of LDS at l
+// (wave-uniform), lane i at l + 16 i.  Written as inline asm: the compiler's
+// form of this load makes it assume every such load may overwrite every
+// other one's LDS bytes, and it then waits for the whole load queue before
+// each of them.  Completion is tracked by the explicit vmcnt waits below.
+// M0 (the LDS address of the load) is restored afterwards, so code the
+// compiler generates around the statement sees it unchanged.
+__device__ __forceinline__ void dma16(const void* g, uint8_t* l) {
+  const uint32_t loff = (uint32_t)(uintptr_t)(lds_u8_t*)(l);
+  uint32_t saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved)
+               : "v"(g), "s"(__builtin_amdgcn_readfirstlane(loff))
+               : "memory");
+}
+
+// Weight row (matrix, row) of tile row tr (0..255).
+template <int NMAT>
+__device__ __forceinline__ void tile_row(int tr, int row0, int N, int& mat, int& row) {
+  if constexpr (NMAT == 2) {
+    mat = tr >> 7;
+    row = row0 + (tr & 127);
+  } else {
+    mat = 0;
+    row = row0 + tr;
+  }
+  row = row < N ? row : N - 1;     // rows past N load row N-1 and are not stored
+}
+
+template <int NMAT, int BM>
+__global__ __launch_bounds__(kThreads, 1) void gemm_ring_kernel(RingArgs a) {
+  using C = RingCfg<BM>;
+  constexpr int kRowsOut = NMAT == 2 ? 128 : 256;   // output rows per tile
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+
+  // ---- tile (XCD-aware: each XCD walks a contiguous range of tiles, token
+  // tiles fastest, so the WGs sharing a weight tile run on one L2) -------
+  const int nwg = gridDim.x;
+  const int wg = blockIdx.x;
+  int logical = wg;
+  if ((nwg & 7) == 0) logical = (wg & 7) * (nwg >> 3) + (wg >> 3);
+  const int n_tile = logical / a.m_tiles;
+  const int m_tile = logical - n_tile * a.m_tiles;
+  const int row0 = n_tile * kRowsOut;
+  const int tok0 = m_tile * BM;
+  const int M = a.M, N = a.N, K = a.K;
+  const int nk = K / kBK;
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int wr = wave & 3;          // row group
+  const int wt = wave >> 2;         // token half
+  const int l32 = lane & 31;
+  const int j = lane >> 5;
+
+  // ---- loads of one stage (this wave's share) ---------------------------
+  // X: instruction q covers token rows 8q .. 8q+7 of the tile.
+  auto issue_stage = [&](int k) {
+    uint8_t* st = smem + (k % kStages) * C::kStage;
+    const int k0 = k * kBK;
+#pragma unroll
+    for (int i = 0; i < C::kXInst; ++i) {
+      const int q = wave + kNW * i;
+      const int tr = 8 * q + (lane >> 3);
+      const int slot = lane & 7;
+      const int c = slot ^ ((tr >> 1) & 7);
+      int tok = tok0 + tr;
+      tok = tok < M ? tok : M - 1;
+      dma16(a.x + (int64_t)tok * K + k0 + 8 * c, st + q * 1024);
+    }
+    {
+      // W: wave w covers tile rows 32w .. 32w+31, two 16-byte halves each
+      const int tr = 32 * wave + (lane >> 1);
+      const int h = (lane & 1) ^ ((tr >> 3) & 1);
+      int mat, row;
+      tile_row<NMAT>(tr, row0, N, mat, row);
+      dma16(a.w[mat] + (int64_t)row * (K / 2) + k0 / 2 + 16 * h, st + C::kXBytes + wave * 1024);
+    }
+    if ((k & 7) == 0) {
+      // scale bytes of 8 steps: tile row tr's 16 bytes; lanes 0..31 of wave w
+      // cover rows 32w .. 32w+31
+      if (lane < 32) {
+        const int tr = 32 * wave + lane;
+        int mat, row;
+        tile_row<NMAT>(tr, row0, N, mat, row);
+        dma16(a.s[mat] + (int64_t)row * (K / 32) + 2 * k, smem + kStages * C::kStage + ((k >> 3) & 1) * kSBlock + wave * 512);
+      }
+    }
+  };
+  // loads per wave of stage k (what vmcnt counts)
+  auto loads_of = [&](int k) { return C::kXInst + 1 + ((k & 7) == 0 ? 1 : 0); };
+
+  f32x16_t acc[2][C::kTT];
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int t = 0; t < C::kTT; ++t)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[b][t][v] = 0.f;
+
+  // this lane's operand rows
+  int wtr[2];                     // tile weight row of block b
+#pragma unroll
+  for (int b = 0; b < 2; ++b) wtr[b] = NMAT == 2 ? b * 128 + wr * 32 + l32 : wr * 64 + b * 32 + l32;
+  int xtr[C::kTT];                // tile token row of block t
+#pragma unroll
+  for (int t = 0; t < C::kTT; ++t) xtr[t] = wt * (BM / 2) + t * 32 + l32;
+
+  issue_stage(0);
+  if (nk > 1) issue_stage(1);
+
+  for (int k = 0; k < nk; ++k) {
+    // this wave's loads of stage k are done when at most stage k+1's remain
+    if (k + 1 < nk) {
+      if (loads_of(k + 1) == C::kXInst + 2) __builtin_amdgcn_s_waitcnt(0x0F70 | (C::kXInst + 2));
+      else __builtin_amdgcn_s_waitcnt(0x0F70 | (C::kXInst + 1));
+    } else {
+      __builtin_amdgcn_s_waitcnt(0x0F70);       // vmcnt(0)
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();               // all waves: stage k landed, step k-1 done
+    asm volatile("" ::: "memory");
+    if (k + 2 < nk) issue_stage(k + 2);
+
+    const uint8_t* st = smem + (k % kStages) * C::kStage;
+    const uint8_t* sb = smem + kStages * C::kStage + ((k >> 3) & 1) * kSBlock;
+    // W operands (16 B packed per block) and scale bytes
+    u32x4_t wraw[2];
+    uint32_t wsc[2];
+    bool ok = true;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int tr = wtr[b];
+      wraw[b] = *reinterpret_cast<const u32x4_t*>(st + C::kXBytes + tr * 32 + 16 * (j ^ ((tr >> 3) & 1)));
+      wsc[b] = sb[tr * 16 + 2 * (k & 7) + j];
+      ok = ok && e8m0_fast_ok(wsc[b]);
+    }
+    // X operands of MFMA k-step s, one 16-byte read per token block
+    auto load_x = [&](int s, u32x4_t (&xo)[C::kTT]) {
+#pragma unroll
+      for (int t = 0; t < C::kTT; ++t) {
+        const int tr = xtr[t];
+        xo[t] = *reinterpret_cast<const u32x4_t*>(st + tr * 128 + 16 * ((4 * j + s) ^ ((tr >> 1) & 7)));
+      }
+    };
+    // k-steps in order with the next k-step's X reads in flight; the
+    // scheduling barriers keep the compiler from hoisting all four k-steps'
+    // reads (64 more live VGPRs at BM = 256).  The exact dequantisation (a
+    // scale byte outside [2, 252], wave-uniform and rare) rewrites only the
+    // two converted operands: a branch around the MFMAs themselves made the
+    // compiler keep two copies of the accumulators.
+    const bool fast = wave_all(ok);
+    u32x4_t xa[C::kTT], xb[C::kTT];
+    load_x(0, xa);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      u32x4_t (&xc)[C::kTT] = (s & 1) ? xb : xa;
+      u32x4_t (&xn)[C::kTT] = (s & 1) ? xa : xb;
+      if (s < 3) load_x(s + 1, xn);
+      u32x4_t wop[2];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) wop[b] = dq8_bf16_fast(wraw[b][s], wsc[b]);
+      if (!fast) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b) wop[b] = dq8_bf16_exact(wraw[b][s], wsc[b]);
+      }
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int t = 0; t < C::kTT; ++t) acc[b][t] = mfma32x32x16(wop[b], xc[t], acc[b][t]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // ---- epilogue --------------------------------------------------------
+  // acc[b][t][v]: token tok0 + xtr[t], tile row block base + 8 (v/4) + 4 j + (v%4)
+#pragma unroll
+  for (int t = 0; t < C::kTT; ++t) {
+    const int tok = tok0 + xtr[t];
+    if (tok >= M) continue;
+#pragma unroll
+    for (int b = 0; b < (NMAT == 2 ? 1 : 2); ++b) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int orow = row0 + (NMAT == 2 ? wr * 32 : wr * 64 + b * 32) + 8 * g + 4 * j;
+        if (orow >= N) continue;   // N % 32 == 0: the 4 rows are all in or all out
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if constexpr (NMAT == 2) v[e] = silu_f32(acc[0][t][4 * g + e]) * acc[1][t][4 * g + e];
+          else v[e] = acc[b][t][4 * g + e];
+        }
+        const uint32_t lo = (uint32_t)f32_to_act<kBF16>(v[0]) | ((uint32_t)f32_to_act<kBF16>(v[1]) << 16);
+        const uint32_t hi = (uint32_t)f32_to_act<kBF16>(v[2]) | ((uint32_t)f32_to_act<kBF16>(v[3]) << 16);
+        *reinterpret_cast<u32x2_t*>(a.out + (int64_t)tok * N + orow) = u32x2_t{lo, hi};
+      }
+    }
+  }
+}
+
+template <int NMAT, int BM>
+hipError_t launch_ring(RingArgs r, hipStream_t st) {
+  using C = RingCfg<BM>;
+  constexpr int kRowsOut = NMAT == 2 ? 128 : 256;
+  r.m_tiles = (r.M + BM - 1) / BM;
+  r.n_tiles = (r.N + kRowsOut - 1) / kRowsOut;
+  const int64_t nwg = (int64_t)r.m_tiles * r.n_tiles;
+  if (nwg > 0x7fffffff) return hipErrorInvalidValue;
+  auto kern = gemm_ring_kernel<NMAT, BM>;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          C::kLds) != hipSuccess) {
+    (void)hipGetLastError();
+    return hipErrorNotSupported;
+  }
+  kern<<<(unsigned)nwg, kThreads, C::kLds, st>>>(r);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool gemm_ring_supported(const MlpArgs& a, int stage) {
+  if (a.dtype != kBF16) return false;
+  if ((stage & kStageGateUp) && a.hidden % 512 != 0) return false;
+  if ((stage & kStageDown) && a.inter % 512 != 0) return false;
+  if (a.n > (1 << 24) || a.hidden > (1 << 20) || a.inter > (1 << 22)) return false;
+  const void* scales[] = {a.gate_scale, a.up_scale, a.down_scale};
+  for (const void* p : scales)
+    if (p && (reinterpret_cast<uintptr_t>(p) & 15u)) return false;
+  int dev = 0;
+  hipDeviceProp_t prop;
+  if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess) return false;
+  return (int64_t)prop.sharedMemPerBlock >= RingCfg<256>::kLds;
+}
+
+hipError_t launch_gemm_ring_mlp(const MlpArgs& a, int stage, hipStream_t st) {
+  if (stage & kStageGateUp) {
+    RingArgs r{static_cast<const uint16_t*>(a.x), {a.gate, a.up}, {a.gate_scale, a.up_scale},
+               static_cast<uint16_t*>(a.tmp), (int)a.n, (int)a.inter, (int)a.hidden, 0, 0};
+    const hipError_t e = launch_ring<2, 256>(r, st);
+    if (e != hipSuccess) return e;
+  }
+  if (stage & kStageDown) {
+    RingArgs r{static_cast<const uint16_t*>(a.tmp), {a.down, a.down}, {a.down_scale, a.down_scale},
+               static_cast<uint16_t*>(a.out), (int)a.n, (int)a.hidden, (int)a.inter, 0, 0};
+    return launch_ring<1, 128>(r, st);
+  }
+  return hipSuccess;
+}
+
+}  // namespace tinyinfer

@@ -35,6 +35,12 @@ hipError_t launch_skinny_mlp(const MlpArgs& a, int stage, hipStream_t stream);
 // Tiled MFMA GEMM path (n >= 128 preferred; any n >= 1 is correct).
 hipError_t launch_gemm_mlp(const MlpArgs& a, int stage, hipStream_t stream);
 
+// Prefill GEMM with a three-stage direct-to-LDS ring (bf16 activations, the
+// stage's K a multiple of 512, 16-byte aligned scale rows); launch_gemm_mlp
+// serves the other GEMM-path calls.
+bool gemm_ring_supported(const MlpArgs& a, int stage);
+hipError_t launch_gemm_ring_mlp(const MlpArgs& a, int stage, hipStream_t stream);
+
 // Streaming decode GEMV kernels (n <= 8): one launch per stage, contiguous
 // load front across the chip.  stream_supported() says whether the call's
 // shape, alignment and LDS needs fit; launch_stream_mlp must only be called
