@@ -34,6 +34,7 @@
 // (a permutation of K shared by both operands leaves each dot product
 // unchanged).  A lane's W bytes for the step are then one 16-byte run under
 // one scale byte, and its X bytes one 64-byte run.
+#include <cstdlib>
 #include <type_traits>
 
 #include "mxfp4_common.hpp"
@@ -293,7 +294,8 @@ hipError_t launch_ring(RingArgs r, hipStream_t st) {
 }  // namespace
 
 bool gemm_ring_supported(const MlpArgs& a, int stage) {
-  if (a.dtype != kBF16) return false;
+  static const bool off = [] { const char* e = std::getenv("TINYINFER_GEMM_RING"); return e && e[0] == '0'; }();
+  if (off || a.dtype != kBF16) return false;
   if ((stage & kStageGateUp) && a.hidden % 512 != 0) return false;
   if ((stage & kStageDown) && a.inter % 512 != 0) return false;
   if (a.n > (1 << 24) || a.hidden > (1 << 20) || a.inter > (1 << 22)) return false;
