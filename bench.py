@@ -61,6 +61,8 @@ def parse():
                    help="only run a 256 MiB device copy (calibrates rocprof FETCH/WRITE_SIZE)")
     p.add_argument("--only", choices=["decode", "gate_up", "down", "prefill"], default=None,
                    help="run a single timed loop (for rocprofv3 runs)")
+    p.add_argument("--path", type=int, default=0,
+                   help="kernel path for --only runs (0 auto, 1 skinny/stream, 2 GEMM, 3 fused decode)")
     return p.parse_args()
 
 
@@ -278,7 +280,7 @@ def main():
     if args.only:
         kind = {"decode": "mlp", "gate_up": "gate_up", "down": "down", "prefill": "mlp"}[args.only]
         mm = args.prefill_m if args.only == "prefill" else m
-        r = Runner(capi, activations(mm, shape.hidden, device="cuda"), sets, kind)
+        r = Runner(capi, activations(mm, shape.hidden, device="cuda"), sets, kind, path=args.path)
         for s in range(args.warmup):
             r.step(s)
         torch.cuda.synchronize()

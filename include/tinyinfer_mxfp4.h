@@ -49,7 +49,7 @@ extern "C" {
 #define TI_PATH_AUTO 0            /* same choice as tinyinfer_mlp_forward_mxfp4 */
 #define TI_PATH_SKINNY 1          /* dequant skinny-GEMM on MFMA (weights streamed once per 64 tokens) */
 #define TI_PATH_GEMM 2            /* LDS-tiled dequant -> bf16 MFMA GEMM */
-#define TI_PATH_DECODE 3          /* fused single-launch decode kernel (N <= 8, full MLP only) */
+#define TI_PATH_DECODE 3          /* fused single-launch decode kernel (N <= 4, full MLP only) */
 
 /* Quantizer flag bits written to *flags by tinyinfer_mxfp4_quantize. */
 #define TI_QFLAG_NONFINITE 1u     /* NaN/Inf in the input */
@@ -64,12 +64,12 @@ extern "C" {
  * with the same arguments in the same order, plus `stream`; errors are
  * returned instead of thrown. `tmp` must hold N*intermediate elements of the
  * activation dtype; on return it holds bf16/fp16 SiLU(g)*u, as in the
- * reference. The kernel path is chosen from N: for N <= 8 the fused
- * single-launch decode kernel when the shape allows it (hidden and
- * intermediate multiples of 256, everything fitting in LDS), else the skinny
- * path up to N < 96, else the tiled GEMM. X, gate, up, down and tmp must be
- * 16-byte aligned. Calls that use the fused decode kernel must not overlap on
- * one device (it synchronizes its workgroups through device memory).
+ * reference. The kernel path is chosen from N: for N <= 8 the streaming
+ * decode kernels (one launch per stage) when hidden and intermediate are
+ * multiples of 512 and the shape fits their LDS plan, else the skinny kernels
+ * up to N < 96, else the tiled GEMM. X, gate, up, down and tmp must be
+ * 16-byte aligned. Calls of the fused decode path (TI_PATH_DECODE) must not
+ * overlap on one device (its workgroups synchronise through device memory).
  */
 int tinyinfer_mlp_forward_mxfp4(const void* X, const uint8_t* gate, const uint8_t* gate_scale,
                                 const uint8_t* up, const uint8_t* up_scale, const uint8_t* down,
@@ -136,9 +136,10 @@ int tinyinfer_mxfp4_quantize(const void* w, int in_dtype, size_t rows, size_t k,
 
 /*
  * Diagnostics of the current device (synchronous): the number of times the
- * fused decode kernel's grid barrier gave up waiting since the library was
- * loaded (a safety bound that only trips if its workgroups were not all
- * resident; results of such a call are invalid). No reference counterpart.
+ * fused decode kernel's wait for the other workgroups gave up since the
+ * library was loaded (a safety bound that only trips if its workgroups were
+ * not all resident; results of such a call are invalid). No reference
+ * counterpart.
  */
 int tinyinfer_mxfp4_diagnostics(uint32_t* decode_barrier_timeouts);
 

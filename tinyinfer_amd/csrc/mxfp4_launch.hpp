@@ -48,12 +48,12 @@ hipError_t launch_gemm_ring_mlp(const MlpArgs& a, int stage, hipStream_t stream)
 bool stream_supported(const MlpArgs& a, int stage);
 hipError_t launch_stream_mlp(const MlpArgs& a, int stage, hipStream_t stream);
 
-// Fused persistent decode kernel (gate_up, grid barrier, down in one launch)
-// for n <= 8 tokens; hipErrorNotSupported when the shape, alignment or the
-// device's LDS/occupancy do not allow it (the caller then uses the skinny path).
+// Fused decode kernel (gate_up, cross-workgroup flags, down in one launch)
+// for n <= 4 tokens; hipErrorNotSupported when the shape, alignment or the
+// device's LDS/occupancy do not allow it.
 hipError_t launch_decode_mlp(const MlpArgs& a, hipStream_t stream);
 
-// Grid-barrier spin timeouts of the fused decode kernel since load (0 unless a
+// Spin timeouts of the fused decode kernel's wait since load (0 unless a
 // workgroup was not resident); synchronous.
 unsigned int decode_barrier_timeouts();
 

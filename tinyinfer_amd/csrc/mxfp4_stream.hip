@@ -460,8 +460,10 @@ bool stream_xreg_allowed(bool gateup) {
 }
 
 // Geometry of one stage; false when the streaming kernel does not apply.
+// force_grid > 0 fixes the grid (the fused decode kernel runs both stages on
+// the gate_up stage's grid).
 bool plan(int64_t M, int64_t K, int64_t R, bool gateup, bool bf16, const DevCaps& d, StreamArgs& a, int& grid,
-          int64_t& lds) {
+          int64_t& lds, int force_grid = 0) {
   // K % 512: a row group's scale rows split into whole 16-byte chunks
   if (d.cus < 1 || M < 1 || M > 8 || K % (2 * kItemK) != 0 || R % 8 != 0) return false;
   if (K > (1 << 20) || R > (1 << 24)) return false;
@@ -475,7 +477,7 @@ bool plan(int64_t M, int64_t K, int64_t R, bool gateup, bool bf16, const DevCaps
   a.spu = stream_spu(gateup, spw);
   a.parts = (spw + a.spu - 1) / a.spu;
   a.rgroups = (int)(R / 8);
-  grid = d.cus < a.rgroups ? d.cus : a.rgroups;
+  grid = force_grid > 0 ? force_grid : (d.cus < a.rgroups ? d.cus : a.rgroups);
   a.nrg_max = (a.rgroups + grid - 1) / grid;
   a.xs_stride = (int)(2 * K + 16);
   a.ss_stride = (int)(K / 32 + 16);
@@ -534,6 +536,443 @@ hipError_t run_stage(const uint16_t* x, const uint8_t* w0, const uint8_t* s0, co
   return launch<DT, GATEUP>(a, lds, grid, st);
 }
 
+// ===================================================================== fused
+//
+// Fused decode (TI_PATH_DECODE, and AUTO for M <= 4): both stages in one
+// launch, one workgroup per CU, all resident.  Phase 1 is the gate_up stream
+// above; each workgroup then publishes its rows of h with agent-scope stores
+// (performed at the device's coherence point, so other XCDs' L2s never hold
+// them) and, once they have completed, sets its flag to the launch's epoch.
+// Before waiting for the other workgroups' flags it issues all of its down
+// weight loads (at most 4 units per wave, registers only), so the down
+// weights stream while the slowest workgroups finish gate_up.  It then reads
+// h with agent-scope loads into LDS and runs the down stream from registers.
+//
+// The flags hold the epoch of the last launch that reached them, so they are
+// never reset: a launch reads the epoch E, waits for flag == E + 1, and
+// workgroup 0 stores E + 1 as the new epoch after its own wait (by then every
+// workgroup has read E).  The wait is a bounded spin: if it ever gives up
+// (workgroups not all resident), the timeout is counted and the launch's
+// results are invalid, but the kernel ends.  Launches must not overlap on a
+// device.
+constexpr int kFusedMaxGrid = 1024;
+constexpr int kFusedMaxUnits2 = 4;
+__device__ uint32_t g_fused_flags[kFusedMaxGrid];
+__device__ uint32_t g_fused_epoch;
+__device__ uint32_t g_fused_timeouts;
+
+struct FusedArgs {
+  StreamArgs g;           // gate_up: x -> h (g.out is tmp)
+  StreamArgs d;           // down: h -> out
+  uint32_t spin_limit;
+};
+
+__device__ __forceinline__ uint32_t agent_load(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// After a row group: partials into its LDS slot, count, and the last wave of
+// the workgroup to get here runs the epilogue into outs.
+template <int DT, bool GATEUP>
+__device__ __forceinline__ void finish_row_group(const StreamArgs& a, float* red, unsigned int* cnt,
+                                                 uint16_t* outs, int li, int wave, const f32x4_t (&acc)[2]) {
+  constexpr int kMats = GATEUP ? 2 : 1;
+  const int lane = threadIdx.x & 63;
+  float* slot = red + (int64_t)li * (kNW * kMats * 64);
+#pragma unroll
+  for (int m = 0; m < kMats; ++m) store_partial(acc[m], slot + (wave * kMats + m) * 64, a.M);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  unsigned int old = 0;
+  if (lane == 0) old = __hip_atomic_fetch_add(&cnt[li], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+  old = __shfl(old, 0, 64);
+  if (old == kNW - 1) {
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    if (lane < 8 * a.M) {
+      const int t = lane >> 3, r = lane & 7;
+      float y0 = 0.f, y1 = 0.f;
+      for (int w = 0; w < kNW; ++w) {
+        y0 += slot[(w * kMats + 0) * 64 + t * 8 + r];
+        if (GATEUP) y1 += slot[(w * kMats + 1) * 64 + t * 8 + r];
+      }
+      const float v = GATEUP ? silu_f32(y0) * y1 : y0;
+      outs[(li * a.M + t) * 8 + r] = f32_to_act<DT>(v);
+    }
+  }
+}
+
+template <int DT, int SPU1, int SPU2, bool XREG1>
+__global__ __launch_bounds__(kNW * 64, 1) void fused_kernel(FusedArgs f) {
+  constexpr int kItems1 = 2 * SPU1;
+  constexpr int kItems2 = SPU2;
+  constexpr int kThreads = kNW * 64;
+  const StreamArgs& A = f.g;
+  const StreamArgs& B = f.d;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int G = gridDim.x;
+  const int g = blockIdx.x;
+  const int q8 = lane >> 3;
+  const uint32_t epoch = __builtin_amdgcn_readfirstlane(agent_load(&g_fused_epoch));
+
+  // phase 1 LDS (x, scales, partials, counters, outputs) from 0; phase 2's
+  // scale rows at B.lds_scl (past both phases' other areas); phase 2's x (h),
+  // partials, counters and outputs from 0 again once phase 1 is done.
+  uint8_t* scl1 = lds + A.lds_scl;
+  float* red1 = reinterpret_cast<float*>(lds + A.lds_red);
+  unsigned int* cnt1 = reinterpret_cast<unsigned int*>(lds + A.lds_cnt);
+  uint16_t* outs1 = reinterpret_cast<uint16_t*>(lds + A.lds_out);
+  uint8_t* scl2 = lds + B.lds_scl;
+  float* red2 = reinterpret_cast<float*>(lds + B.lds_red);
+  unsigned int* cnt2 = reinterpret_cast<unsigned int*>(lds + B.lds_cnt);
+  uint16_t* outs2 = reinterpret_cast<uint16_t*>(lds + B.lds_out);
+
+  const int P1 = A.parts, P2 = B.parts;
+  const int nrg1 = (A.rgroups - g + G - 1) / G;
+  const int units1 = nrg1 * P1;
+  const int nrg2 = g < B.rgroups ? (B.rgroups - g + G - 1) / G : 0;
+  const int units2 = nrg2 * P2;
+  const int tok = ((lane & 15) & 7) < A.M ? ((lane & 15) & 7) : A.M - 1;
+  int lo1, hi1;
+  seg_run(A, wave, lo1, hi1);
+
+  for (int i = threadIdx.x; i < A.nrg_max; i += kThreads) cnt1[i] = 0u;
+
+  // ---- prologue: x, phase 1 and phase 2 scale rows -> LDS ---------------
+  const int x_row = A.K / 8;
+  const int nxc = A.M * x_row;
+  auto x_src = [&](int c) {
+    const int cc = c < nxc ? c : nxc - 1;
+    const int t = cc / x_row, k8 = cc - t * x_row;
+    return reinterpret_cast<const u32x4_t*>(A.x + (int64_t)t * A.K + 8 * k8);
+  };
+  auto x_dst = [&](int c) {
+    const int t = c / x_row, k8 = c - t * x_row;
+    return reinterpret_cast<u32x4_t*>(lds + t * A.xs_stride + 16 * k8);
+  };
+  // scale chunk c of a stage: block (li, mat) = c / (K/64): rows rg*8 ..
+  // rg*8+7 of that matrix, contiguous in memory
+  const int sb1 = A.K / 64, nsc1 = nrg1 * 2 * sb1;
+  const int sb2 = B.K / 64, nsc2 = nrg2 * sb2;
+  auto s1_src = [&](int c) {
+    const int cc = c < nsc1 ? c : nsc1 - 1;
+    const int blk = cc / sb1, off = 16 * (cc - blk * sb1);
+    const int li = blk >> 1, mat = blk & 1;
+    return reinterpret_cast<const u32x4_t*>((mat ? A.s1 : A.s0) + (int64_t)(g + li * G) * 8 * (A.K / 32) + off);
+  };
+  auto s1_dst = [&](int c) {
+    const int blk = c / sb1, off = 16 * (c - blk * sb1);
+    const int row = off / (A.K / 32), col = off - row * (A.K / 32);
+    return reinterpret_cast<u32x4_t*>(scl1 + (blk * 8 + row) * A.ss_stride + col);
+  };
+  auto s2_src = [&](int c) {
+    const int cc = c < nsc2 ? c : (nsc2 > 0 ? nsc2 - 1 : 0);
+    const int li = cc / sb2, off = 16 * (cc - li * sb2);
+    const int rg = nsc2 > 0 ? g + li * G : 0;
+    return reinterpret_cast<const u32x4_t*>(B.s0 + (int64_t)rg * 8 * (B.K / 32) + off);
+  };
+  auto s2_dst = [&](int c) {
+    const int li = c / sb2, off = 16 * (c - li * sb2);
+    const int row = off / (B.K / 32), col = off - row * (B.K / 32);
+    return reinterpret_cast<u32x4_t*>(scl2 + (li * 8 + row) * B.ss_stride + col);
+  };
+  auto sync_copy = [&](int n, int pre, auto src, auto dst) {
+    for (int c0 = threadIdx.x + pre * kThreads; c0 < n; c0 += 4 * kThreads) {
+      u32x4_t v[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) v[b] = *src(c0 + b * kThreads);
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        if (c0 + b * kThreads < n) *dst(c0 + b * kThreads) = v[b];
+    }
+  };
+  sync_copy(nxc, kXPre, x_src, x_dst);
+  sync_copy(nsc1, kSPre, s1_src, s1_dst);
+  sync_copy(nsc2, 2, s2_src, s2_dst);
+  u32x4_t xv[kXPre], sv1[kSPre], sv2[2];
+#pragma unroll
+  for (int b = 0; b < kXPre; ++b) xv[b] = *x_src(threadIdx.x + b * kThreads);
+#pragma unroll
+  for (int b = 0; b < kSPre; ++b) sv1[b] = *s1_src(threadIdx.x + b * kThreads);
+  if (nsc2 > 0) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) sv2[b] = *s2_src(threadIdx.x + b * kThreads);
+  }
+
+  struct Buf1 {
+    u32x4_t w[kItems1];
+  };
+  Buf1 a0, a1;
+  auto issue1 = [&](Buf1& b, int u) {
+    const int uu = u < units1 ? u : units1 - 1;    // past the end: repeat the last unit's loads
+    const int rgi = uu / P1, part = uu - rgi * P1;
+    issue_unit<SPU1, true>(A, g + rgi * G, part, wave, b.w);
+  };
+  issue1(a0, 0);
+  issue1(a1, 1);
+
+#pragma unroll
+  for (int b = 0; b < kXPre; ++b)
+    if (threadIdx.x + b * kThreads < nxc) *x_dst(threadIdx.x + b * kThreads) = xv[b];
+#pragma unroll
+  for (int b = 0; b < kSPre; ++b)
+    if (threadIdx.x + b * kThreads < nsc1) *s1_dst(threadIdx.x + b * kThreads) = sv1[b];
+  if (nsc2 > 0) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+      if (threadIdx.x + b * kThreads < nsc2) *s2_dst(threadIdx.x + b * kThreads) = sv2[b];
+  }
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);    // lgkmcnt(0): LDS stores done, weights stay in flight
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+
+  // ---- phase 1: gate_up -------------------------------------------------
+  const uint8_t* xrow1 = lds + tok * A.xs_stride;
+  constexpr int kNX = XREG1 ? SPU1 : 1;
+  u32x4_t xr[kNX][4];
+  if constexpr (XREG1) {
+#pragma unroll
+    for (int j = 0; j < kNX; ++j) {
+      const int seg = lo1 + j < A.segs ? lo1 + j : A.segs - 1;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        xr[j][t] = *reinterpret_cast<const u32x4_t*>(xrow1 + 2 * (seg * kItemK + 32 * q8 + 8 * t));
+    }
+  }
+  f32x4_t acc[2];
+  auto step1 = [&](Buf1& b, int u) {
+    const int rgi = u / P1, part = u - rgi * P1;
+    if (part == 0) acc[0] = acc[1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    if constexpr (XREG1) {
+      auto xf = [&](int sg, int t) { return xr[sg][t]; };
+      compute_unit<DT, SPU1, true>(A, wave, rgi, 0, b.w, scl1, xf, acc);
+    } else {
+      auto xf = [&](int sg, int t) {
+        int s0, nu;
+        unit_segs(A, wave, part, SPU1, s0, nu);
+        return *reinterpret_cast<const u32x4_t*>(xrow1 + 2 * ((s0 + sg) * kItemK + 32 * q8 + 8 * t));
+      };
+      compute_unit<DT, SPU1, true>(A, wave, rgi, part, b.w, scl1, xf, acc);
+    }
+    issue1(b, u + 2);
+    if (part == P1 - 1) finish_row_group<DT, true>(A, red1, cnt1, outs1, rgi, wave, acc);
+  };
+  int u = 0;
+  for (; u + 1 < units1; u += 2) {
+    step1(a0, u);
+    step1(a1, u + 1);
+  }
+  if (u < units1) step1(a0, u);
+
+  // ---- publish this workgroup's rows of h, then its flag ---------------
+  __syncthreads();
+  {
+    // outs1 [li][t][8 rows] bf16: 16 bytes per (li, t), two 8-byte stores
+    const int n8 = nrg1 * A.M * 2;
+    for (int i = threadIdx.x; i < n8; i += kThreads) {
+      const int lt = i >> 1, half = i & 1;
+      const int li = lt / A.M, t = lt - li * A.M;
+      const uint64_t v = *reinterpret_cast<const uint64_t*>(outs1 + lt * 8 + 4 * half);
+      uint64_t* dst = reinterpret_cast<uint64_t*>(A.out + (int64_t)t * A.R + (int64_t)(g + li * G) * 8 + 4 * half);
+      __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);     // this thread's stores (and loads) have completed
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_store(&g_fused_flags[g], epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (units2 == 0) return;           // no down rows here; workgroup 0 always has some
+
+  // ---- phase 2: down ------------------------------------------------------
+  for (int i = threadIdx.x; i < B.nrg_max; i += kThreads) cnt2[i] = 0u;
+  struct Buf2 {
+    u32x4_t w[kItems2];
+  };
+  Buf2 b0, b1, b2, b3;
+  auto issue2 = [&](Buf2& b, int v) {
+    const int vv = v < units2 ? v : units2 - 1;
+    const int rgi = vv / P2, part = vv - rgi * P2;
+    issue_unit<SPU2, false>(B, g + rgi * G, part, wave, b.w);
+  };
+  // Waves 1..7 put their down loads in flight now; wave 0 first polls the
+  // flags, since its poll loads would otherwise return only after its own
+  // down loads (loads complete in issue order).
+  if (wave != 0) {
+    issue2(b0, 0);
+    issue2(b1, 1);
+    issue2(b2, 2);
+    issue2(b3, 3);
+  }
+
+  // every workgroup's h rows: wave 0 polls the flags (bounded)
+  if (wave == 0) {
+    const uint32_t want = epoch + 1u;
+    for (uint32_t it = 0;; ++it) {
+      bool done = true;
+      for (int i = lane; i < G; i += 64) done = done && agent_load(&g_fused_flags[i]) == want;
+      if (wave_all(done)) break;
+      if (it >= f.spin_limit) {
+        if (lane == 0) __hip_atomic_fetch_add(&g_fused_timeouts, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    issue2(b0, 0);
+    issue2(b1, 1);
+    issue2(b2, 2);
+    issue2(b3, 3);
+  }
+  __syncthreads();
+  if (g == 0 && threadIdx.x == 0)
+    __hip_atomic_store(&g_fused_epoch, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  // h [M, I] -> LDS rows of B.xs_stride bytes, 8-byte agent-scope loads
+  {
+    const int per_row = B.K / 4;
+    const int n8 = B.M * per_row;
+    for (int i = threadIdx.x; i < n8; i += kThreads) {
+      const int t = i / per_row, c = i - t * per_row;
+      const uint64_t v = __hip_atomic_load(reinterpret_cast<const uint64_t*>(B.x + (int64_t)t * B.K + 4 * c),
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *reinterpret_cast<uint64_t*>(lds + t * B.xs_stride + 8 * c) = v;
+    }
+  }
+  __syncthreads();
+
+  // down's activations for this wave's K range (at most 2 parts of SPU2
+  // segments) in VGPRs, copied once: reading LDS per MFMA made the multiply
+  // LDS-bound.  With 4-segment units that would not fit; those read LDS.
+  constexpr bool kXReg2 = SPU2 <= 3;
+  const uint8_t* xrow2 = lds + tok * B.xs_stride;
+  int lo2, hi2;
+  seg_run(B, wave, lo2, hi2);
+  u32x4_t xr2[kXReg2 ? 2 * SPU2 : 1][4];
+  if constexpr (kXReg2) {
+#pragma unroll
+    for (int j = 0; j < 2 * SPU2; ++j) {
+      const int seg = lo2 + j < B.segs ? lo2 + j : B.segs - 1;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        xr2[j][t] = *reinterpret_cast<const u32x4_t*>(xrow2 + 2 * (seg * kItemK + 32 * q8 + 8 * t));
+    }
+  }
+  auto step2 = [&](Buf2& b, int v) {
+    const int rgi = v / P2, part = v - rgi * P2;
+    if (part == 0) acc[0] = acc[1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    if constexpr (kXReg2) {
+      auto run = [&](auto part_tag) {
+        constexpr int PT = decltype(part_tag)::value;
+        auto xf = [&](int sg, int t) { return xr2[PT * SPU2 + sg][t]; };
+        compute_unit<DT, SPU2, false>(B, wave, rgi, PT, b.w, scl2, xf, acc);
+      };
+      if (part == 0) run(std::integral_constant<int, 0>{});
+      else run(std::integral_constant<int, 1>{});
+    } else {
+      auto xf = [&](int sg, int t) {
+        int s0, nu;
+        unit_segs(B, wave, part, SPU2, s0, nu);
+        return *reinterpret_cast<const u32x4_t*>(xrow2 + 2 * ((s0 + sg) * kItemK + 32 * q8 + 8 * t));
+      };
+      compute_unit<DT, SPU2, false>(B, wave, rgi, part, b.w, scl2, xf, acc);
+    }
+    if (part == P2 - 1) finish_row_group<DT, false>(B, red2, cnt2, outs2, rgi, wave, acc);
+  };
+  step2(b0, 0);
+  if (units2 > 1) step2(b1, 1);
+  if (units2 > 2) step2(b2, 2);
+  if (units2 > 3) step2(b3, 3);
+
+  __syncthreads();
+  for (int i = threadIdx.x; i < nrg2 * B.M * 8; i += kThreads) {
+    const int li = i / (B.M * 8), rem = i - li * B.M * 8;
+    const int t = rem >> 3, r = rem & 7;
+    B.out[(int64_t)t * B.R + (int64_t)(g + li * G) * 8 + r] = outs2[i];
+  }
+}
+
+// Geometry of a fused launch; false when it does not apply.
+bool plan_fused(const MlpArgs& m, const DevCaps& d, FusedArgs& f, int& grid, int64_t& lds) {
+  if (m.n < 1 || m.n > 4 || d.cus < 1) return false;
+  const bool bf = m.dtype == kBF16;
+  int64_t l1 = 0, l2 = 0;
+  if (!plan(m.n, m.hidden, m.inter, true, bf, d, f.g, grid, l1)) return false;
+  if (grid > kFusedMaxGrid) return false;
+  int grid2 = 0;
+  if (!plan(m.n, m.inter, m.hidden, false, bf, d, f.d, grid2, l2, grid)) return false;
+  if (f.d.nrg_max * f.d.parts > kFusedMaxUnits2 || f.d.parts > 2) return false;
+  // phase 1: [x][scl1][red1][cnt1][out1] as planned; phase 2 reuses the start
+  // for [h][red2][cnt2][out2]; phase 2's scale rows after both
+  StreamArgs& B = f.d;
+  const int64_t p1 = l1;
+  const int64_t h_bytes = (int64_t)m.n * B.xs_stride;
+  B.lds_red = (int)h_bytes;
+  B.lds_cnt = B.lds_red + B.nrg_max * kNW * 64 * 4;
+  B.lds_out = B.lds_cnt + 4 * ((B.nrg_max + 3) & ~3);
+  const int64_t p2 = B.lds_out + (int64_t)B.nrg_max * m.n * 8 * 2;
+  B.lds_scl = (int)(((p1 > p2 ? p1 : p2) + 15) & ~int64_t(15));
+  lds = B.lds_scl + (int64_t)B.nrg_max * 8 * B.ss_stride;
+  if (lds > d.max_lds) return false;
+  f.spin_limit = 1u << 20;
+  return true;
+}
+
+template <int DT>
+hipError_t run_fused(const MlpArgs& m, hipStream_t st) {
+  const DevCaps d = caps();
+  FusedArgs f;
+  int grid = 0;
+  int64_t lds = 0;
+  if (!plan_fused(m, d, f, grid, lds)) return hipErrorNotSupported;
+  const void* p16[] = {m.x, m.gate, m.up, m.down, m.tmp, m.gate_scale, m.up_scale, m.down_scale};
+  for (const void* p : p16)
+    if (!aligned16(p)) return hipErrorNotSupported;
+  f.g.x = static_cast<const uint16_t*>(m.x);
+  f.g.w0 = m.gate;
+  f.g.s0 = m.gate_scale;
+  f.g.w1 = m.up;
+  f.g.s1 = m.up_scale;
+  f.g.out = static_cast<uint16_t*>(m.tmp);
+  f.d.x = static_cast<const uint16_t*>(m.tmp);
+  f.d.w0 = f.d.w1 = m.down;
+  f.d.s0 = f.d.s1 = m.down_scale;
+  f.d.out = static_cast<uint16_t*>(m.out);
+  auto go = [&](auto kern) -> hipError_t {
+    if (lds > 64 * 1024 &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lds) != hipSuccess) {
+      (void)hipGetLastError();
+      return hipErrorNotSupported;
+    }
+    // every workgroup must be resident at once
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kNW * 64, (size_t)lds) != hipSuccess ||
+        per_cu < 1) {
+      (void)hipGetLastError();
+      return hipErrorNotSupported;
+    }
+    if ((int64_t)per_cu * d.cus < grid) return hipErrorNotSupported;
+    kern<<<grid, kNW * 64, (size_t)lds, st>>>(f);
+    return hipGetLastError();
+  };
+  auto pick2 = [&](auto s1_tag, auto xr_tag) -> hipError_t {
+    constexpr int S1 = decltype(s1_tag)::value;
+    constexpr bool XR = decltype(xr_tag)::value;
+    switch (f.d.spu) {
+      case 1: return go(fused_kernel<DT, S1, 1, XR>);
+      case 2: return go(fused_kernel<DT, S1, 2, XR>);
+      case 3: return go(fused_kernel<DT, S1, 3, XR>);
+      default: return go(fused_kernel<DT, S1, 4, XR>);
+    }
+  };
+  const bool xreg = DT == kBF16 && f.g.xreg;
+  if (f.g.spu <= 1) {
+    return xreg ? pick2(std::integral_constant<int, 1>{}, std::true_type{})
+                : pick2(std::integral_constant<int, 1>{}, std::false_type{});
+  }
+  return xreg ? pick2(std::integral_constant<int, 2>{}, std::true_type{})
+              : pick2(std::integral_constant<int, 2>{}, std::false_type{});
+}
+
 }  // namespace
 
 bool stream_supported(const MlpArgs& a, int stage) {
@@ -568,6 +1007,17 @@ hipError_t launch_stream_mlp(const MlpArgs& a, int stage, hipStream_t st) {
               : run_stage<kF16, false>(h, a.down, a.down_scale, nullptr, nullptr, a.n, a.inter, a.hidden, y, st);
   }
   return hipSuccess;
+}
+
+hipError_t launch_decode_mlp(const MlpArgs& a, hipStream_t st) {
+  if (a.n > 4) return hipErrorNotSupported;
+  return a.dtype == kBF16 ? run_fused<kBF16>(a, st) : run_fused<kF16>(a, st);
+}
+
+unsigned int decode_barrier_timeouts() {
+  unsigned int v = 0;
+  if (hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_fused_timeouts), sizeof(v)) != hipSuccess) return 0xffffffffu;
+  return v;
 }
 
 }  // namespace tinyinfer
