@@ -6,7 +6,12 @@ Each stage is called through its C-ABI entry point and compared with the CPU
 oracle at the kernel's rounding points (exact sums, h rounded once to the
 activation dtype): a few bf16 ulps. Cases: partial token tiles, the Qwen3
 block shapes, scale bytes outside the hardware conversion's exact range,
-fp16 activations (register-staged kernel), bit-reproducibility."""
+fp16 activations (register-staged kernel), bit-reproducibility, and the
+split-K form of the ring kernels (fp32 partials over K ranges summed in a
+fixed order by a reduce kernel) that runs when the output tiles alone would
+leave CUs idle.""" 
+
+import os
 
 import numpy as np
 import pytest
@@ -97,3 +102,37 @@ def test_gemm_deterministic_and_full_call(capi):
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
     assert torch.equal(a.view(torch.int16), c.view(torch.int16))
     check_close(a.cpu(), om.mlp_kernel_semantics(x, *mats), "1.7B m=300 full")
+
+
+@pytest.mark.parametrize("m", [96, 128, 384])
+def test_gemm_split_k_qwen3_8b(capi, m):
+    """Qwen3-8B shapes at token counts whose tiles leave CUs idle: down has 16
+    output tiles per 128 tokens, so its K (12288) is split."""
+    banner(f"gemm split-K qwen3-8b m={m}")
+    x, mats = make_case(m, 4096, 12288, seed=77 + m)
+    run_gemm_stages(capi, x, mats, f"8B m={m}")
+
+
+@pytest.mark.parametrize("ksplit", [1, 2, 3, 5])
+def test_gemm_forced_split_counts(capi, ksplit, monkeypatch):
+    """Every split count gives the oracle's result within tolerance, also
+    uneven ranges (5 ranges over 6 blocks of 512 K) and no split at all."""
+    monkeypatch.setenv("TINYINFER_RING_KSPLIT", str(ksplit))
+    banner(f"gemm forced ksplit={ksplit}")
+    x, mats = make_case(200, 3072, 3072, seed=600 + ksplit)
+    run_gemm_stages(capi, x, mats, f"ksplit={ksplit}")
+
+
+def test_gemm_split_deterministic(capi, monkeypatch):
+    """Split results are bit-reproducible and close to the unsplit ones."""
+    banner("gemm split determinism")
+    x, mats = make_case(160, 2048, 6144, seed=31)
+    xd, md = to_dev(x, mats)
+    monkeypatch.setenv("TINYINFER_RING_KSPLIT", "4")
+    a = capi.mlp_forward(xd, *md, path=GEMM)
+    b = capi.mlp_forward(xd, *md, path=GEMM)
+    monkeypatch.setenv("TINYINFER_RING_KSPLIT", "1")
+    c = capi.mlp_forward(xd, *md, path=GEMM)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    check_close(a.cpu(), c.cpu().float(), "split vs unsplit")

@@ -35,7 +35,10 @@
 // unchanged).  A lane's W bytes for the step are then one 16-byte run under
 // one scale byte, and its X bytes one 64-byte run.
 #include <cstdlib>
+#include <map>
+#include <mutex>
 #include <type_traits>
+#include <utility>
 
 #include "mxfp4_common.hpp"
 #include "mxfp4_launch.hpp"
@@ -71,6 +74,8 @@ struct RingArgs {
   uint16_t* out;            // [M, N]
   int M, N, K;              // N: output rows
   int m_tiles, n_tiles;
+  float* ws;                // split K: fp32 partials [ksplit][M][NMAT * N]
+  int ksplit;               // K ranges per tile (1: no split)
 };
 
 // 64 lanes x 16 bytes from per-lane global addresses to 1 KB of LDS at l
@@ -102,7 +107,11 @@ __device__ __forceinline__ void tile_row(int tr, int row0, int N, int& mat, int&
   row = row < N ? row : N - 1;     // rows past N load row N-1 and are not stored
 }
 
-template <int NMAT, int BM>
+// SPLIT: the grid also splits K into ksplit ranges of whole 8-step blocks
+// (the scale staging's granularity); each workgroup writes its fp32 partial
+// tile to the workspace, and ring_reduce sums the ranges in a fixed order and
+// applies the epilogue.  Used when the tiles alone would leave CUs idle.
+template <int NMAT, int BM, bool SPLIT>
 __global__ __launch_bounds__(kThreads, 1) void gemm_ring_kernel(RingArgs a) {
   using C = RingCfg<BM>;
   constexpr int kRowsOut = NMAT == 2 ? 128 : 256;   // output rows per tile
@@ -114,12 +123,17 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_ring_kernel(RingArgs a) {
   const int wg = blockIdx.x;
   int logical = wg;
   if ((nwg & 7) == 0) logical = (wg & 7) * (nwg >> 3) + (wg >> 3);
-  const int n_tile = logical / a.m_tiles;
-  const int m_tile = logical - n_tile * a.m_tiles;
+  const int tile = SPLIT ? logical / a.ksplit : logical;
+  const int ks = SPLIT ? logical - tile * a.ksplit : 0;
+  const int n_tile = tile / a.m_tiles;
+  const int m_tile = tile - n_tile * a.m_tiles;
   const int row0 = n_tile * kRowsOut;
   const int tok0 = m_tile * BM;
   const int M = a.M, N = a.N, K = a.K;
-  const int nk = K / kBK;
+  // K steps [kbeg, kend) of this workgroup
+  const int nblk = K / (8 * kBK);
+  const int kbeg = SPLIT ? 8 * (ks * nblk / a.ksplit) : 0;
+  const int kend = SPLIT ? 8 * ((ks + 1) * nblk / a.ksplit) : K / kBK;
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -131,7 +145,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_ring_kernel(RingArgs a) {
   // ---- loads of one stage (this wave's share) ---------------------------
   // X: instruction q covers token rows 8q .. 8q+7 of the tile.
   auto issue_stage = [&](int k) {
-    uint8_t* st = smem + (k % kStages) * C::kStage;
+    uint8_t* st = smem + ((k - kbeg) % kStages) * C::kStage;
     const int k0 = k * kBK;
 #pragma unroll
     for (int i = 0; i < C::kXInst; ++i) {
@@ -181,12 +195,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_ring_kernel(RingArgs a) {
 #pragma unroll
   for (int t = 0; t < C::kTT; ++t) xtr[t] = wt * (BM / 2) + t * 32 + l32;
 
-  issue_stage(0);
-  if (nk > 1) issue_stage(1);
+  issue_stage(kbeg);
+  if (kbeg + 1 < kend) issue_stage(kbeg + 1);
 
-  for (int k = 0; k < nk; ++k) {
+  for (int k = kbeg; k < kend; ++k) {
     // this wave's loads of stage k are done when at most stage k+1's remain
-    if (k + 1 < nk) {
+    if (k + 1 < kend) {
       if (loads_of(k + 1) == C::kXInst + 2) __builtin_amdgcn_s_waitcnt(0x0F70 | (C::kXInst + 2));
       else __builtin_amdgcn_s_waitcnt(0x0F70 | (C::kXInst + 1));
     } else {
@@ -195,9 +209,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_ring_kernel(RingArgs a) {
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();               // all waves: stage k landed, step k-1 done
     asm volatile("" ::: "memory");
-    if (k + 2 < nk) issue_stage(k + 2);
+    if (k + 2 < kend) issue_stage(k + 2);
 
-    const uint8_t* st = smem + (k % kStages) * C::kStage;
+    const uint8_t* st = smem + ((k - kbeg) % kStages) * C::kStage;
     const uint8_t* sb = smem + kStages * C::kStage + ((k >> 3) & 1) * kSBlock;
     // W operands (16 B packed per block) and scale bytes
     u32x4_t wraw[2];
@@ -249,6 +263,27 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_ring_kernel(RingArgs a) {
 
   // ---- epilogue --------------------------------------------------------
   // acc[b][t][v]: token tok0 + xtr[t], tile row block base + 8 (v/4) + 4 j + (v%4)
+  if constexpr (SPLIT) {
+    // fp32 partials: [ks][token][mat * N + row], four consecutive rows per store
+#pragma unroll
+    for (int t = 0; t < C::kTT; ++t) {
+      const int tok = tok0 + xtr[t];
+      if (tok >= M) continue;
+      float* wrow = a.ws + ((int64_t)ks * M + tok) * (NMAT * N);
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int orow = row0 + (NMAT == 2 ? wr * 32 : wr * 64 + b * 32) + 8 * g + 4 * j;
+          if (orow >= N) continue;
+          const int col = (NMAT == 2 ? b * N : 0) + orow;
+          *reinterpret_cast<f32x4_t*>(wrow + col) =
+              f32x4_t{acc[b][t][4 * g], acc[b][t][4 * g + 1], acc[b][t][4 * g + 2], acc[b][t][4 * g + 3]};
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int t = 0; t < C::kTT; ++t) {
     const int tok = tok0 + xtr[t];
@@ -273,21 +308,119 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_ring_kernel(RingArgs a) {
   }
 }
 
+// out[m][n] = epilogue(sum over ks of ws[ks][m][n] (and [N + n] for up)), in
+// ks order; four outputs per thread.
+template <int NMAT>
+__global__ __launch_bounds__(256) void ring_reduce(const float* __restrict__ ws, uint16_t* __restrict__ out,
+                                                   int M, int N, int ksplit) {
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;   // group of 4 outputs
+  const int64_t total = (int64_t)M * N / 4;
+  if (q >= total) return;
+  const int64_t m = q / (N / 4);
+  const int n = (int)(q - m * (N / 4)) * 4;
+  f32x4_t g = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
+  for (int ks = 0; ks < ksplit; ++ks) {
+    const float* row = ws + ((int64_t)ks * M + m) * (NMAT * N);
+    g += *reinterpret_cast<const f32x4_t*>(row + n);
+    if constexpr (NMAT == 2) u += *reinterpret_cast<const f32x4_t*>(row + N + n);
+  }
+  float v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = NMAT == 2 ? silu_f32(g[e]) * u[e] : g[e];
+  const uint32_t lo = (uint32_t)f32_to_act<kBF16>(v[0]) | ((uint32_t)f32_to_act<kBF16>(v[1]) << 16);
+  const uint32_t hi = (uint32_t)f32_to_act<kBF16>(v[2]) | ((uint32_t)f32_to_act<kBF16>(v[3]) << 16);
+  *reinterpret_cast<u32x2_t*>(out + m * N + n) = u32x2_t{lo, hi};
+}
+
+// Split-K workspace: one buffer per (device, stream), grown on demand and
+// kept (calls on one stream are ordered, so they can share it).  Growth is
+// refused during graph capture (the caller then runs without splitting).
+float* split_workspace(size_t bytes, hipStream_t st) {
+  static std::mutex mu;
+  static std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> bufs;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  auto& b = bufs[{dev, st}];
+  if (b.second >= bytes) return static_cast<float*>(b.first);
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  const size_t want = (bytes + (64u << 20) - 1) & ~size_t((64u << 20) - 1);
+  if (b.first) {
+    // kernels of this stream may still read the old buffer
+    if (hipStreamSynchronize(st) != hipSuccess) return nullptr;
+    (void)hipFree(b.first);
+    b = {nullptr, 0};
+  }
+  void* p = nullptr;
+  if (hipMalloc(&p, want) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  b = {p, want};
+  return static_cast<float*>(p);
+}
+
+// Number of K ranges per output tile.  Cost model (microseconds): a tile's
+// full-K time at ~5 TFLOP/s per CU, times the rounds of workgroups the split
+// grid needs on 256 CUs, divided by the split; plus the fp32 partials written
+// and read back (mostly from the 256 MB last-level cache) and the reduce
+// launch.  The smallest split with the least cost wins; K ranges are whole
+// 8-step blocks.  TINYINFER_RING_KSPLIT=<n> forces n (clamped), for tuning.
+int ring_ksplit(const RingArgs& r, int bm, int nmat, int64_t tiles) {
+  const int nblk = r.K / (8 * kBK);
+  int cap = nblk < 32 ? nblk : 32;
+  if (const char* e = std::getenv("TINYINFER_RING_KSPLIT")) {
+    const int v = std::atoi(e);
+    if (v >= 1) return v < cap ? v : (cap > 0 ? cap : 1);
+  }
+  const double t_tile = 2.0 * bm * 256.0 * r.K / 5e6;
+  const double ws_us_per_split = 8.0 * r.M * nmat * (double)r.N / 8e6;
+  int best = 1;
+  double best_cost = t_tile * (double)((tiles + 255) / 256);
+  for (int ks = 2; ks <= cap; ++ks) {
+    const double rounds = (double)((tiles * ks + 255) / 256);
+    const double cost = t_tile * rounds / ks + ws_us_per_split * ks + 3.0;
+    if (cost < best_cost * 0.97) {
+      best = ks;
+      best_cost = cost;
+    }
+  }
+  return best;
+}
+
 template <int NMAT, int BM>
 hipError_t launch_ring(RingArgs r, hipStream_t st) {
   using C = RingCfg<BM>;
   constexpr int kRowsOut = NMAT == 2 ? 128 : 256;
   r.m_tiles = (r.M + BM - 1) / BM;
   r.n_tiles = (r.N + kRowsOut - 1) / kRowsOut;
-  const int64_t nwg = (int64_t)r.m_tiles * r.n_tiles;
-  if (nwg > 0x7fffffff) return hipErrorInvalidValue;
-  auto kern = gemm_ring_kernel<NMAT, BM>;
-  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                          C::kLds) != hipSuccess) {
-    (void)hipGetLastError();
-    return hipErrorNotSupported;
+  const int64_t tiles = (int64_t)r.m_tiles * r.n_tiles;
+  if (tiles > 0x7fffffff / 32) return hipErrorInvalidValue;
+  const int ksplit_want = ring_ksplit(r, BM, NMAT, tiles);
+  int ksplit = 1;
+  if (ksplit_want > 1) {
+    r.ws = split_workspace((size_t)ksplit_want * r.M * NMAT * r.N * sizeof(float), st);
+    if (r.ws) ksplit = ksplit_want;
   }
-  kern<<<(unsigned)nwg, kThreads, C::kLds, st>>>(r);
+  r.ksplit = ksplit;
+  auto go = [&](auto kern, int64_t nwg) -> hipError_t {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            C::kLds) != hipSuccess) {
+      (void)hipGetLastError();
+      return hipErrorNotSupported;
+    }
+    kern<<<(unsigned)nwg, kThreads, C::kLds, st>>>(r);
+    return hipGetLastError();
+  };
+  if (ksplit == 1) return go(gemm_ring_kernel<NMAT, BM, false>, tiles);
+  const hipError_t e = go(gemm_ring_kernel<NMAT, BM, true>, tiles * ksplit);
+  if (e != hipSuccess) return e;
+  const int64_t groups = (int64_t)r.M * r.N / 4;
+  ring_reduce<NMAT><<<(unsigned)((groups + 255) / 256), 256, 0, st>>>(r.ws, r.out, r.M, r.N, ksplit);
   return hipGetLastError();
 }
 
@@ -302,22 +435,29 @@ bool gemm_ring_supported(const MlpArgs& a, int stage) {
   const void* scales[] = {a.gate_scale, a.up_scale, a.down_scale};
   for (const void* p : scales)
     if (p && (reinterpret_cast<uintptr_t>(p) & 15u)) return false;
+  static int64_t lds_cache[64] = {};
   int dev = 0;
-  hipDeviceProp_t prop;
-  if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess) return false;
-  return (int64_t)prop.sharedMemPerBlock >= RingCfg<256>::kLds;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+  if (lds_cache[dev] == 0) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return false;
+    lds_cache[dev] = (int64_t)prop.sharedMemPerBlock;
+  }
+  return lds_cache[dev] >= RingCfg<256>::kLds;
 }
 
 hipError_t launch_gemm_ring_mlp(const MlpArgs& a, int stage, hipStream_t st) {
   if (stage & kStageGateUp) {
     RingArgs r{static_cast<const uint16_t*>(a.x), {a.gate, a.up}, {a.gate_scale, a.up_scale},
-               static_cast<uint16_t*>(a.tmp), (int)a.n, (int)a.inter, (int)a.hidden, 0, 0};
-    const hipError_t e = launch_ring<2, 256>(r, st);
+               static_cast<uint16_t*>(a.tmp), (int)a.n, (int)a.inter, (int)a.hidden, 0, 0, nullptr, 1};
+    // 256-token tiles once there are enough of them (more reuse of each
+    // weight tile), 128 below
+    const hipError_t e = a.n > 1024 ? launch_ring<2, 256>(r, st) : launch_ring<2, 128>(r, st);
     if (e != hipSuccess) return e;
   }
   if (stage & kStageDown) {
     RingArgs r{static_cast<const uint16_t*>(a.tmp), {a.down, a.down}, {a.down_scale, a.down_scale},
-               static_cast<uint16_t*>(a.out), (int)a.n, (int)a.hidden, (int)a.inter, 0, 0};
+               static_cast<uint16_t*>(a.out), (int)a.n, (int)a.hidden, (int)a.inter, 0, 0, nullptr, 1};
     return launch_ring<1, 128>(r, st);
   }
   return hipSuccess;
