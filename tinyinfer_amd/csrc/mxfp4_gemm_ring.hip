@@ -50,21 +50,21 @@ namespace {
 typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
 
 constexpr int kBK = 64;           // K per step
-constexpr int kNW = 8;            // waves
-constexpr int kThreads = kNW * 64;
 constexpr int kWRows = 256;       // weight rows per tile
 constexpr int kWBytes = kWRows * 32;      // packed W per stage
 constexpr int kSBlock = kWRows * 16;      // scale bytes per 8-step block
 constexpr int kStages = 3;
 
-template <int BM>
+template <int BM, int NW>
 struct RingCfg {
   static constexpr int kXBytes = BM * 2 * kBK;                 // X per stage
   static constexpr int kStage = kXBytes + kWBytes;
   static constexpr int kLds = kStages * kStage + 2 * kSBlock;
-  static constexpr int kXInst = BM / 8 / kNW;                  // X loads per wave per stage
-  static constexpr int kTT = BM / 64;                          // 32-token blocks per wave
-  static_assert(kXInst >= 1 && kXInst * 8 * kNW == BM, "token tile must split over the waves");
+  static constexpr int kXInst = BM / 8 / NW;                   // X loads per wave per stage
+  static constexpr int kWInst = 8 / NW;                        // W loads per wave per stage
+  static constexpr int kSRows = kWRows / NW;                   // scale rows per wave (one per lane)
+  static_assert(kXInst >= 1 && kXInst * 8 * NW == BM, "token tile must split over the waves");
+  static_assert(kWInst >= 1 && kSRows <= 64, "4 or 8 waves");
 };
 
 struct RingArgs {
@@ -111,9 +111,22 @@ __device__ __forceinline__ void tile_row(int tr, int row0, int N, int& mat, int&
 // (the scale staging's granularity); each workgroup writes its fp32 partial
 // tile to the workspace, and ring_reduce sums the ranges in a fixed order and
 // applies the epilogue.  Used when the tiles alone would leave CUs idle.
-template <int NMAT, int BM, bool SPLIT>
-__global__ __launch_bounds__(kThreads, 1) void gemm_ring_kernel(RingArgs a) {
-  using C = RingCfg<BM>;
+// WR: waves along the weight rows (8 / WR along the tokens).  A wave holds
+// WB = 8 / WR blocks of 32 weight rows and kTT = BM / 32 / (8 / WR) blocks of
+// 32 tokens; fewer, wider weight blocks per wave read less LDS per MFMA (the
+// packed weights are a quarter of the bytes of the activations) at the cost
+// of more conversions.
+// NW: waves per workgroup.  8 waves run one workgroup per CU; 4 waves with
+// 128-token tiles fit two workgroups per CU, whose barriers are independent.
+template <int NMAT, int BM, bool SPLIT, int WR, int NW>
+__global__ __launch_bounds__(NW * 64, 2) void gemm_ring_kernel(RingArgs a) {
+  using C = RingCfg<BM, NW>;
+  constexpr int WT = NW / WR;                  // waves along the tokens
+  constexpr int WB = 8 / WR;                   // weight blocks per wave
+  static_assert(WR * WT == NW, "wave grid");
+  constexpr int kTT = BM / 32 / WT;            // token blocks per wave
+  constexpr int kRowsW = kWRows / WR;          // tile rows per wave (both matrices)
+  static_assert(kTT >= 1 && kTT * 32 * WT == BM, "token tile must split over the waves");
   constexpr int kRowsOut = NMAT == 2 ? 128 : 256;   // output rows per tile
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
@@ -137,8 +150,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_ring_kernel(RingArgs a) {
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  const int wr = wave & 3;          // row group
-  const int wt = wave >> 2;         // token half
+  const int wr = wave % WR;         // row group
+  const int wt = wave / WR;         // token group
   const int l32 = lane & 31;
   const int j = lane >> 5;
 
@@ -149,7 +162,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_ring_kernel(RingArgs a) {
     const int k0 = k * kBK;
 #pragma unroll
     for (int i = 0; i < C::kXInst; ++i) {
-      const int q = wave + kNW * i;
+      const int q = wave + NW * i;
       const int tr = 8 * q + (lane >> 3);
       const int slot = lane & 7;
       const int c = slot ^ ((tr >> 1) & 7);
@@ -157,43 +170,52 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_ring_kernel(RingArgs a) {
       tok = tok < M ? tok : M - 1;
       dma16(a.x + (int64_t)tok * K + k0 + 8 * c, st + q * 1024);
     }
-    {
-      // W: wave w covers tile rows 32w .. 32w+31, two 16-byte halves each
-      const int tr = 32 * wave + (lane >> 1);
+#pragma unroll
+    for (int i = 0; i < C::kWInst; ++i) {
+      // W: instruction qi covers tile rows 32 qi .. 32 qi + 31, two 16-byte halves each
+      const int qi = wave * C::kWInst + i;
+      const int tr = 32 * qi + (lane >> 1);
       const int h = (lane & 1) ^ ((tr >> 3) & 1);
       int mat, row;
       tile_row<NMAT>(tr, row0, N, mat, row);
-      dma16(a.w[mat] + (int64_t)row * (K / 2) + k0 / 2 + 16 * h, st + C::kXBytes + wave * 1024);
+      dma16(a.w[mat] + (int64_t)row * (K / 2) + k0 / 2 + 16 * h, st + C::kXBytes + qi * 1024);
     }
     if ((k & 7) == 0) {
-      // scale bytes of 8 steps: tile row tr's 16 bytes; lanes 0..31 of wave w
-      // cover rows 32w .. 32w+31
-      if (lane < 32) {
-        const int tr = 32 * wave + lane;
+      // scale bytes of 8 steps: tile row tr's 16 bytes; lane l of wave w
+      // covers row kSRows w + l
+      if (lane < C::kSRows) {
+        const int tr = C::kSRows * wave + lane;
         int mat, row;
         tile_row<NMAT>(tr, row0, N, mat, row);
-        dma16(a.s[mat] + (int64_t)row * (K / 32) + 2 * k, smem + kStages * C::kStage + ((k >> 3) & 1) * kSBlock + wave * 512);
+        dma16(a.s[mat] + (int64_t)row * (K / 32) + 2 * k,
+              smem + kStages * C::kStage + ((k >> 3) & 1) * kSBlock + wave * C::kSRows * 16);
       }
     }
   };
-  // loads per wave of stage k (what vmcnt counts)
-  auto loads_of = [&](int k) { return C::kXInst + 1 + ((k & 7) == 0 ? 1 : 0); };
+  // loads per wave of a stage (what vmcnt counts): one more every 8 steps
+  constexpr int kLoads = C::kXInst + C::kWInst;
+  static_assert(kLoads + 1 <= 15, "vmcnt immediate");
 
-  f32x16_t acc[2][C::kTT];
+  f32x16_t acc[WB][kTT];
 #pragma unroll
-  for (int b = 0; b < 2; ++b)
+  for (int b = 0; b < WB; ++b)
 #pragma unroll
-    for (int t = 0; t < C::kTT; ++t)
+    for (int t = 0; t < kTT; ++t)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[b][t][v] = 0.f;
 
   // this lane's operand rows
-  int wtr[2];                     // tile weight row of block b
+  // tile weight row of block b: gate_up blocks are [gate 0 .. WB/2-1][up ...]
+  // over the same output rows, so the epilogue has g and u in one lane
+  int wtr[WB];
 #pragma unroll
-  for (int b = 0; b < 2; ++b) wtr[b] = NMAT == 2 ? b * 128 + wr * 32 + l32 : wr * 64 + b * 32 + l32;
-  int xtr[C::kTT];                // tile token row of block t
+  for (int b = 0; b < WB; ++b) {
+    if constexpr (NMAT == 2) wtr[b] = (b / (WB / 2)) * 128 + wr * (kRowsW / 2) + (b % (WB / 2)) * 32 + l32;
+    else wtr[b] = wr * kRowsW + b * 32 + l32;
+  }
+  int xtr[kTT];                   // tile token row of block t
 #pragma unroll
-  for (int t = 0; t < C::kTT; ++t) xtr[t] = wt * (BM / 2) + t * 32 + l32;
+  for (int t = 0; t < kTT; ++t) xtr[t] = wt * (BM / WT) + t * 32 + l32;
 
   issue_stage(kbeg);
   if (kbeg + 1 < kend) issue_stage(kbeg + 1);
@@ -201,8 +223,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_ring_kernel(RingArgs a) {
   for (int k = kbeg; k < kend; ++k) {
     // this wave's loads of stage k are done when at most stage k+1's remain
     if (k + 1 < kend) {
-      if (loads_of(k + 1) == C::kXInst + 2) __builtin_amdgcn_s_waitcnt(0x0F70 | (C::kXInst + 2));
-      else __builtin_amdgcn_s_waitcnt(0x0F70 | (C::kXInst + 1));
+      if (((k + 1) & 7) == 0) __builtin_amdgcn_s_waitcnt(0x0F70 | (kLoads + 1));
+      else __builtin_amdgcn_s_waitcnt(0x0F70 | kLoads);
     } else {
       __builtin_amdgcn_s_waitcnt(0x0F70);       // vmcnt(0)
     }
@@ -214,20 +236,20 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_ring_kernel(RingArgs a) {
     const uint8_t* st = smem + ((k - kbeg) % kStages) * C::kStage;
     const uint8_t* sb = smem + kStages * C::kStage + ((k >> 3) & 1) * kSBlock;
     // W operands (16 B packed per block) and scale bytes
-    u32x4_t wraw[2];
-    uint32_t wsc[2];
+    u32x4_t wraw[WB];
+    uint32_t wsc[WB];
     bool ok = true;
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
+    for (int b = 0; b < WB; ++b) {
       const int tr = wtr[b];
       wraw[b] = *reinterpret_cast<const u32x4_t*>(st + C::kXBytes + tr * 32 + 16 * (j ^ ((tr >> 3) & 1)));
       wsc[b] = sb[tr * 16 + 2 * (k & 7) + j];
       ok = ok && e8m0_fast_ok(wsc[b]);
     }
     // X operands of MFMA k-step s, one 16-byte read per token block
-    auto load_x = [&](int s, u32x4_t (&xo)[C::kTT]) {
+    auto load_x = [&](int s, u32x4_t (&xo)[kTT]) {
 #pragma unroll
-      for (int t = 0; t < C::kTT; ++t) {
+      for (int t = 0; t < kTT; ++t) {
         const int tr = xtr[t];
         xo[t] = *reinterpret_cast<const u32x4_t*>(st + tr * 128 + 16 * ((4 * j + s) ^ ((tr >> 1) & 7)));
       }
@@ -239,24 +261,24 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_ring_kernel(RingArgs a) {
     // two converted operands: a branch around the MFMAs themselves made the
     // compiler keep two copies of the accumulators.
     const bool fast = wave_all(ok);
-    u32x4_t xa[C::kTT], xb[C::kTT];
+    u32x4_t xa[kTT], xb[kTT];
     load_x(0, xa);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      u32x4_t (&xc)[C::kTT] = (s & 1) ? xb : xa;
-      u32x4_t (&xn)[C::kTT] = (s & 1) ? xa : xb;
+      u32x4_t (&xc)[kTT] = (s & 1) ? xb : xa;
+      u32x4_t (&xn)[kTT] = (s & 1) ? xa : xb;
       if (s < 3) load_x(s + 1, xn);
-      u32x4_t wop[2];
+      u32x4_t wop[WB];
 #pragma unroll
-      for (int b = 0; b < 2; ++b) wop[b] = dq8_bf16_fast(wraw[b][s], wsc[b]);
+      for (int b = 0; b < WB; ++b) wop[b] = dq8_bf16_fast(wraw[b][s], wsc[b]);
       if (!fast) {
 #pragma unroll
-        for (int b = 0; b < 2; ++b) wop[b] = dq8_bf16_exact(wraw[b][s], wsc[b]);
+        for (int b = 0; b < WB; ++b) wop[b] = dq8_bf16_exact(wraw[b][s], wsc[b]);
       }
 #pragma unroll
-      for (int b = 0; b < 2; ++b)
+      for (int b = 0; b < WB; ++b)
 #pragma unroll
-        for (int t = 0; t < C::kTT; ++t) acc[b][t] = mfma32x32x16(wop[b], xc[t], acc[b][t]);
+        for (int t = 0; t < kTT; ++t) acc[b][t] = mfma32x32x16(wop[b], xc[t], acc[b][t]);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -266,17 +288,18 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_ring_kernel(RingArgs a) {
   if constexpr (SPLIT) {
     // fp32 partials: [ks][token][mat * N + row], four consecutive rows per store
 #pragma unroll
-    for (int t = 0; t < C::kTT; ++t) {
+    for (int t = 0; t < kTT; ++t) {
       const int tok = tok0 + xtr[t];
       if (tok >= M) continue;
       float* wrow = a.ws + ((int64_t)ks * M + tok) * (NMAT * N);
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
+      for (int b = 0; b < WB; ++b) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int orow = row0 + (NMAT == 2 ? wr * 32 : wr * 64 + b * 32) + 8 * g + 4 * j;
+          const int orow = row0 + (NMAT == 2 ? wr * (kRowsW / 2) + (b % (WB / 2)) * 32 : wr * kRowsW + b * 32) +
+                           8 * g + 4 * j;
           if (orow >= N) continue;
-          const int col = (NMAT == 2 ? b * N : 0) + orow;
+          const int col = (NMAT == 2 ? (b / (WB / 2)) * N : 0) + orow;
           *reinterpret_cast<f32x4_t*>(wrow + col) =
               f32x4_t{acc[b][t][4 * g], acc[b][t][4 * g + 1], acc[b][t][4 * g + 2], acc[b][t][4 * g + 3]};
         }
@@ -285,19 +308,19 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_ring_kernel(RingArgs a) {
     return;
   }
 #pragma unroll
-  for (int t = 0; t < C::kTT; ++t) {
+  for (int t = 0; t < kTT; ++t) {
     const int tok = tok0 + xtr[t];
     if (tok >= M) continue;
 #pragma unroll
-    for (int b = 0; b < (NMAT == 2 ? 1 : 2); ++b) {
+    for (int b = 0; b < (NMAT == 2 ? WB / 2 : WB); ++b) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int orow = row0 + (NMAT == 2 ? wr * 32 : wr * 64 + b * 32) + 8 * g + 4 * j;
+        const int orow = row0 + (NMAT == 2 ? wr * (kRowsW / 2) : wr * kRowsW) + b * 32 + 8 * g + 4 * j;
         if (orow >= N) continue;   // N % 32 == 0: the 4 rows are all in or all out
         float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          if constexpr (NMAT == 2) v[e] = silu_f32(acc[0][t][4 * g + e]) * acc[1][t][4 * g + e];
+          if constexpr (NMAT == 2) v[e] = silu_f32(acc[b][t][4 * g + e]) * acc[WB / 2 + b][t][4 * g + e];
           else v[e] = acc[b][t][4 * g + e];
         }
         const uint32_t lo = (uint32_t)f32_to_act<kBF16>(v[0]) | ((uint32_t)f32_to_act<kBF16>(v[1]) << 16);
@@ -370,19 +393,21 @@ float* split_workspace(size_t bytes, hipStream_t st) {
 // and read back (mostly from the 256 MB last-level cache) and the reduce
 // launch.  The smallest split with the least cost wins; K ranges are whole
 // 8-step blocks.  TINYINFER_RING_KSPLIT=<n> forces n (clamped), for tuning.
-int ring_ksplit(const RingArgs& r, int bm, int nmat, int64_t tiles) {
+int ring_ksplit(const RingArgs& r, int bm, int nmat, int64_t tiles, int per_cu) {
   const int nblk = r.K / (8 * kBK);
   int cap = nblk < 32 ? nblk : 32;
   if (const char* e = std::getenv("TINYINFER_RING_KSPLIT")) {
     const int v = std::atoi(e);
     if (v >= 1) return v < cap ? v : (cap > 0 ? cap : 1);
   }
-  const double t_tile = 2.0 * bm * 256.0 * r.K / 5e6;
+  // per_cu workgroups share a CU: each runs at 1 / per_cu of its rate
+  const int64_t slots = 256 * per_cu;
+  const double t_tile = 2.0 * bm * 256.0 * r.K / 5e6 * per_cu;
   const double ws_us_per_split = 8.0 * r.M * nmat * (double)r.N / 8e6;
   int best = 1;
-  double best_cost = t_tile * (double)((tiles + 255) / 256);
+  double best_cost = t_tile * (double)((tiles + slots - 1) / slots);
   for (int ks = 2; ks <= cap; ++ks) {
-    const double rounds = (double)((tiles * ks + 255) / 256);
+    const double rounds = (double)((tiles * ks + slots - 1) / slots);
     const double cost = t_tile * rounds / ks + ws_us_per_split * ks + 3.0;
     if (cost < best_cost * 0.97) {
       best = ks;
@@ -392,15 +417,15 @@ int ring_ksplit(const RingArgs& r, int bm, int nmat, int64_t tiles) {
   return best;
 }
 
-template <int NMAT, int BM>
+template <int NMAT, int BM, int WR, int NW = 8>
 hipError_t launch_ring(RingArgs r, hipStream_t st) {
-  using C = RingCfg<BM>;
+  using C = RingCfg<BM, NW>;
   constexpr int kRowsOut = NMAT == 2 ? 128 : 256;
   r.m_tiles = (r.M + BM - 1) / BM;
   r.n_tiles = (r.N + kRowsOut - 1) / kRowsOut;
   const int64_t tiles = (int64_t)r.m_tiles * r.n_tiles;
   if (tiles > 0x7fffffff / 32) return hipErrorInvalidValue;
-  const int ksplit_want = ring_ksplit(r, BM, NMAT, tiles);
+  const int ksplit_want = ring_ksplit(r, BM, NMAT, tiles, NW == 4 ? 2 : 1);
   int ksplit = 1;
   if (ksplit_want > 1) {
     r.ws = split_workspace((size_t)ksplit_want * r.M * NMAT * r.N * sizeof(float), st);
@@ -413,15 +438,25 @@ hipError_t launch_ring(RingArgs r, hipStream_t st) {
       (void)hipGetLastError();
       return hipErrorNotSupported;
     }
-    kern<<<(unsigned)nwg, kThreads, C::kLds, st>>>(r);
+    kern<<<(unsigned)nwg, NW * 64, C::kLds, st>>>(r);
     return hipGetLastError();
   };
-  if (ksplit == 1) return go(gemm_ring_kernel<NMAT, BM, false>, tiles);
-  const hipError_t e = go(gemm_ring_kernel<NMAT, BM, true>, tiles * ksplit);
+  if (ksplit == 1) return go(gemm_ring_kernel<NMAT, BM, false, WR, NW>, tiles);
+  const hipError_t e = go(gemm_ring_kernel<NMAT, BM, true, WR, NW>, tiles * ksplit);
   if (e != hipSuccess) return e;
   const int64_t groups = (int64_t)r.M * r.N / 4;
   ring_reduce<NMAT><<<(unsigned)((groups + 255) / 256), 256, 0, st>>>(r.ws, r.out, r.M, r.N, ksplit);
   return hipGetLastError();
+}
+
+// Wave layout override for tuning: TINYINFER_RING_WR_GU / _DN = 2 or 4.
+int ring_env_wr(const char* name) {
+  const char* e = std::getenv(name);
+  return (e && std::atoi(e) == 2) ? 2 : 4;
+}
+int ring_env_nw(const char* name) {
+  const char* e = std::getenv(name);
+  return (e && std::atoi(e) == 4) ? 4 : 8;
 }
 
 }  // namespace
@@ -443,7 +478,7 @@ bool gemm_ring_supported(const MlpArgs& a, int stage) {
     if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return false;
     lds_cache[dev] = (int64_t)prop.sharedMemPerBlock;
   }
-  return lds_cache[dev] >= RingCfg<256>::kLds;
+  return lds_cache[dev] >= RingCfg<256, 8>::kLds;
 }
 
 hipError_t launch_gemm_ring_mlp(const MlpArgs& a, int stage, hipStream_t st) {
@@ -452,13 +487,21 @@ hipError_t launch_gemm_ring_mlp(const MlpArgs& a, int stage, hipStream_t st) {
                static_cast<uint16_t*>(a.tmp), (int)a.n, (int)a.inter, (int)a.hidden, 0, 0, nullptr, 1};
     // 256-token tiles once there are enough of them (more reuse of each
     // weight tile), 128 below
-    const hipError_t e = a.n > 1024 ? launch_ring<2, 256>(r, st) : launch_ring<2, 128>(r, st);
+    static const int wr = ring_env_wr("TINYINFER_RING_WR_GU");
+    static const int nw = ring_env_nw("TINYINFER_RING_NW_GU");
+    hipError_t e;
+    if (nw == 4) e = wr == 2 ? launch_ring<2, 128, 2, 4>(r, st) : launch_ring<2, 128, 4, 4>(r, st);
+    else if (a.n > 1024) e = wr == 2 ? launch_ring<2, 256, 2>(r, st) : launch_ring<2, 256, 4>(r, st);
+    else e = wr == 2 ? launch_ring<2, 128, 2>(r, st) : launch_ring<2, 128, 4>(r, st);
     if (e != hipSuccess) return e;
   }
   if (stage & kStageDown) {
     RingArgs r{static_cast<const uint16_t*>(a.tmp), {a.down, a.down}, {a.down_scale, a.down_scale},
                static_cast<uint16_t*>(a.out), (int)a.n, (int)a.hidden, (int)a.inter, 0, 0, nullptr, 1};
-    return launch_ring<1, 128>(r, st);
+    static const int wr = ring_env_wr("TINYINFER_RING_WR_DN");
+    static const int nw = ring_env_nw("TINYINFER_RING_NW_DN");
+    if (nw == 4) return wr == 2 ? launch_ring<1, 64, 2, 4>(r, st) : launch_ring<1, 64, 4, 4>(r, st);
+    return wr == 2 ? launch_ring<1, 128, 2>(r, st) : launch_ring<1, 128, 4>(r, st);
   }
   return hipSuccess;
 }
