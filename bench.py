@@ -111,7 +111,9 @@ class Runner:
             self.step(0)                      # first call on this stream outside capture
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
-        with torch.cuda.graph(g):
+        # capture on the warmed stream: the library's split-K workspace for it
+        # exists (allocation cannot happen during capture)
+        with torch.cuda.graph(g, stream=side):
             for s in range(steps):
                 self.step(s)
         torch.cuda.synchronize()

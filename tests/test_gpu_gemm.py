@@ -136,3 +136,48 @@ def test_gemm_split_deterministic(capi, monkeypatch):
     torch.cuda.synchronize()
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
     check_close(a.cpu(), c.cpu().float(), "split vs unsplit")
+
+
+def test_gemm_split_k_graph_replays(capi):
+    """Graphs: on a capture stream that already ran the call eagerly, the
+    split kernels and their workspace are captured, and every replay (with
+    eager work between them) gives the eager bits; on a fresh capture stream
+    the call is captured unsplit, still within tolerance of the oracle."""
+    banner("gemm split-K graph replays")
+    x, mats = make_case(160, 2048, 6144, seed=44)
+    xd, md = to_dev(x, mats)
+    ref = om.mlp_kernel_semantics(x, *mats)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    out = torch.empty((160, 2048), dtype=torch.bfloat16, device="cuda")
+    tmp = torch.empty((160, 6144), dtype=torch.bfloat16, device="cuda")
+    with torch.cuda.stream(s):
+        capi.mlp_forward(xd, *md, out=out, tmp=tmp, path=GEMM)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    eager = out.clone()
+    check_close(eager.cpu(), ref, "eager split")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for _ in range(3):
+            capi.mlp_forward(xd, *md, out=out, tmp=tmp, path=GEMM)
+    for _ in range(4):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), eager.view(torch.int16))
+        capi.mlp_forward(xd, *md, path=GEMM)          # eager work between replays
+        torch.cuda.synchronize()
+    del g
+    g2 = torch.cuda.CUDAGraph()
+    out2 = torch.empty_like(out)
+    with torch.cuda.graph(g2):                        # a fresh capture stream
+        capi.mlp_forward(xd, *md, out=out2, tmp=tmp, path=GEMM)
+    for _ in range(2):
+        out2.zero_()
+        torch.cuda.synchronize()
+        g2.replay()
+        torch.cuda.synchronize()
+        check_close(out2.cpu(), ref, "fresh-stream capture")
+    del g2

@@ -39,6 +39,7 @@
 #include <mutex>
 #include <type_traits>
 #include <utility>
+#include <vector>
 
 #include "mxfp4_common.hpp"
 #include "mxfp4_launch.hpp"
@@ -355,12 +356,18 @@ __global__ __launch_bounds__(256) void ring_reduce(const float* __restrict__ ws,
   *reinterpret_cast<u32x2_t*>(out + m * N + n) = u32x2_t{lo, hi};
 }
 
-// Split-K workspace: one buffer per (device, stream), grown on demand and
-// kept (calls on one stream are ordered, so they can share it).  Growth is
-// refused during graph capture (the caller then runs without splitting).
+// Split-K workspace: one buffer per (device, stream), grown on demand.  A
+// buffer is never freed: a replaced one is kept for the life of the process,
+// because kernels still queued, and graphs captured with it, hold its
+// address.  Growth is refused during graph capture (allocation is not a
+// capturable operation); the call then runs unsplit.  So a graph gets the
+// split kernels when its capture stream has already run a call of at least
+// the same size eagerly (the usual warm-up).  Calls on one stream are
+// ordered, so they share its buffer; calls on other streams use their own.
 float* split_workspace(size_t bytes, hipStream_t st) {
   static std::mutex mu;
   static std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> bufs;
+  static std::vector<void*> retired;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return nullptr;
   std::lock_guard<std::mutex> lock(mu);
@@ -372,17 +379,12 @@ float* split_workspace(size_t bytes, hipStream_t st) {
     return nullptr;
   }
   const size_t want = (bytes + (64u << 20) - 1) & ~size_t((64u << 20) - 1);
-  if (b.first) {
-    // kernels of this stream may still read the old buffer
-    if (hipStreamSynchronize(st) != hipSuccess) return nullptr;
-    (void)hipFree(b.first);
-    b = {nullptr, 0};
-  }
   void* p = nullptr;
   if (hipMalloc(&p, want) != hipSuccess) {
     (void)hipGetLastError();
     return nullptr;
   }
+  if (b.first) retired.push_back(b.first);
   b = {p, want};
   return static_cast<float*>(p);
 }
