@@ -54,7 +54,8 @@ def parse():
     p.add_argument("--m", type=int, default=1, help="headline token count")
     p.add_argument("--prefill-m", type=int, default=2048, help="prefill token count (0: skip)")
     p.add_argument("--prefill-steps", type=int, default=100)
-    p.add_argument("--all", action="store_true", help="also measure every other BASELINE config")
+    p.add_argument("--all", action="store_true",
+                   help="also measure every other BASELINE config (1.7B decode, 8B M=256/512, 32B 64-layer stack)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline sample budget")
     p.add_argument("--copy-probe", action="store_true",
@@ -241,6 +242,50 @@ def measure_point(capi, shape, m, sets, steps, path=0, reps=3):
             "tok_s": round(m / (ms * 1e-3), 1), "steps": steps, "weight_sets": len(sets)}
 
 
+def measure_stack(capi, m, reps=5):
+    """BASELINE's Qwen3-32B config: 64 MLP layers (hidden 5120, intermediate
+    25600, ~13.4 GB of MXFP4 weights, far beyond the MALL) with the residual
+    add between layers; one graph per pass (x reset from x0 inside it)."""
+    import torch
+    from tinyinfer_amd.workloads import SHAPES, activations, alg_bytes, alg_flops, mlp_stack_step, quantized_weights
+    shp = SHAPES["qwen3-32b"]
+    layers = [quantized_weights(shp.hidden, shp.inter, layer=l, generator="cuda") for l in range(shp.layers)]
+    x0 = activations(m, shp.hidden, device="cuda")
+    x = x0.clone()
+    out = torch.empty_like(x0)
+    tmp = torch.empty((m, shp.inter), dtype=x0.dtype, device="cuda")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        mlp_stack_step(capi, x, layers, out, tmp)           # warm-up pass on the capture stream
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        x.copy_(x0)
+        mlp_stack_step(capi, x, layers, out, tmp)
+    g.replay()
+    torch.cuda.synchronize()
+    per = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        per.append(a.elapsed_time(b))
+    del g, layers
+    torch.cuda.empty_cache()
+    ms = statistics.median(per)
+    byt = shp.layers * alg_bytes(m, shp.hidden, shp.inter)
+    fl = shp.layers * alg_flops(m, shp.hidden, shp.inter)
+    return {"config": f"{shp.name} x{shp.layers} layers + residual", "m": m, "ms_per_pass": round(ms, 4),
+            "tok_s": round(m / (ms * 1e-3), 1), "gbs": round(byt / ms / 1e6, 1),
+            "hbm_frac": round(byt / ms / 1e6 / HBM_PEAK_GBS, 4), "tflops": round(fl / ms / 1e9, 2),
+            "mfma_frac": round(fl / ms / 1e9 / BF16_PEAK_TFLOPS, 4), "reps": reps,
+            "note": "residual adds (torch) included in the time"}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -347,6 +392,10 @@ def main():
                 points.append(measure_point(capi, shp, mm, st, 200 if mm <= 8 else 50))
                 log(json.dumps(points[-1]))
             del st
+        torch.cuda.empty_cache()
+        for mm in (1, 512):
+            points.append(measure_stack(capi, mm))
+            log(json.dumps(points[-1]))
 
     cpu = None
     if not args.no_cpu:

@@ -42,7 +42,7 @@ namespace {
 
 constexpr int kNW = 8;            // waves per workgroup
 constexpr int kItemK = 256;       // K elements per item (one 128-byte segment per row)
-constexpr int kMaxSpw = 8;        // max K segments per wave per row group
+constexpr int kMaxSpw = 32;       // max K segments per wave per row group (K <= 65536)
 constexpr int kXPre = 4;          // x chunks per thread loaded ahead of the weights
 constexpr int kSPre = 4;          // scale chunks per thread loaded ahead of the weights
 
@@ -438,17 +438,30 @@ int env_int(const char* name, int dflt, int lo, int hi) {
   return v < lo ? lo : (v > hi ? hi : v);
 }
 
-// Segments per unit for a wave run of up to `spw` segments: the fewest units
-// with at most 4 weight items each (gate_up reads two matrices per segment),
-// spread evenly.  TINYINFER_STREAM_SPU_GU / _DN override it for tuning.
-int stream_spu(bool gateup, int spw) {
-  static const int gu = env_int("TINYINFER_STREAM_SPU_GU", 0, 0, 2);
+// Segments per unit for a wave run of up to `spw` segments: the least of
+// load slots (units x segments per unit, the last unit padded) plus 0.8 slot
+// per unit (its issue, scale reads and pipeline step), at most 3 segments per
+// gate_up unit (6 weight items; 2 for fp16 activations, whose split operands
+// need more registers) and 4 per down unit.  Measured at K = 5120 (3
+// segments per wave): one 3-segment unit beats a 2 + 1 split by 17%.
+// TINYINFER_STREAM_SPU_GU / _DN override it for tuning.
+int stream_spu(bool gateup, bool bf16, int spw) {
+  static const int gu = env_int("TINYINFER_STREAM_SPU_GU", 0, 0, 3);
   static const int dn = env_int("TINYINFER_STREAM_SPU_DN", 0, 0, 4);
   const int forced = gateup ? gu : dn;
-  if (forced > 0) return forced;
-  const int cap = gateup ? 2 : 4;
-  const int parts = (spw + cap - 1) / cap;
-  return (spw + parts - 1) / parts;
+  if (forced > 0) return gateup && !bf16 && forced > 2 ? 2 : forced;
+  const int cap = gateup ? (bf16 ? 3 : 2) : 4;
+  int best = 1;
+  double best_cost = 1.8 * spw;
+  for (int spu = 2; spu <= cap; ++spu) {
+    const int units = (spw + spu - 1) / spu;
+    const double cost = units * spu + 0.8 * units;
+    if (cost < best_cost) {
+      best = spu;
+      best_cost = cost;
+    }
+  }
+  return best;
 }
 
 constexpr int kDepth = 2;         // units in flight per wave
@@ -474,7 +487,7 @@ bool plan(int64_t M, int64_t K, int64_t R, bool gateup, bool bf16, const DevCaps
   a.segs = (int)(K / kItemK);
   const int spw = (a.segs + kNW - 1) / kNW;
   if (spw > kMaxSpw) return false;
-  a.spu = stream_spu(gateup, spw);
+  a.spu = stream_spu(gateup, bf16, spw);
   a.parts = (spw + a.spu - 1) / a.spu;
   a.rgroups = (int)(R / 8);
   grid = force_grid > 0 ? force_grid : (d.cus < a.rgroups ? d.cus : a.rgroups);
@@ -512,6 +525,7 @@ hipError_t launch(const StreamArgs& a, int64_t lds, int grid, hipStream_t st) {
   };
   if (a.spu <= 1) return depth(std::integral_constant<int, 1>{});
   if constexpr (GATEUP) {
+    if (a.spu == 3) return depth(std::integral_constant<int, 3>{});
     return depth(std::integral_constant<int, 2>{});
   } else {
     if (a.spu == 2) return depth(std::integral_constant<int, 2>{});

@@ -84,3 +84,14 @@ def quantized_weights(h: int, i: int, layer: int = 0, generator: str = "cuda", d
 
 def activations(m: int, h: int, dtype=torch.bfloat16, seed: int = X_SEED, generator: str = "cpu", device="cuda"):
     return _randn((m, h), seed, generator, None).to(dtype).to(device)
+
+
+def mlp_stack_step(capi, x, layers, out, tmp):
+    """One pass of the Qwen3-32B MLP stack workload: ``x <- x + MLP_l(x)`` for
+    every layer, in the activation dtype (the residual add is torch's, on the
+    current stream, rounding x + out once as the reference's ``x = x + mlp(x)``
+    does).  ``out``/``tmp`` are [M, H] / [M, I] buffers reused by every layer."""
+    for w in layers:
+        capi.mlp_forward(x, *w, out=out, tmp=tmp)
+        x.add_(out)
+    return x
