@@ -111,6 +111,39 @@ int tinyinfer_mlp_down_mxfp4(const void* tmp, const uint8_t* down, const uint8_t
                              int dtype_code, int path, void* stream);
 
 /*
+ * The MLP followed by the decoder layer's residual add, fused into the down
+ * stage's epilogue: O = residual + MLP(X), where MLP(X) is first rounded to
+ * the activation dtype and the sum is taken in fp32 and rounded again --
+ * bit-identical to tinyinfer_mlp_forward_mxfp4 followed by the reference's
+ * `hidden_states = residual + hidden_states` (tinyinfer/models/qwen3.py:219)
+ * on two activation-dtype tensors, without that extra launch and [N, hidden]
+ * round trip. `residual` is [N, hidden] in the activation dtype, 16-byte
+ * aligned; O may be residual itself (in-place). `path` as in
+ * tinyinfer_mlp_forward_mxfp4_path.
+ */
+int tinyinfer_mlp_forward_mxfp4_residual(const void* X, const uint8_t* gate, const uint8_t* gate_scale,
+                                         const uint8_t* up, const uint8_t* up_scale,
+                                         const uint8_t* down, const uint8_t* down_scale, size_t N,
+                                         size_t hidden_dim, size_t intermediate, void* tmp,
+                                         const void* residual, void* O, int dtype_code, int path,
+                                         void* stream);
+
+/*
+ * One MXFP4 linear layer on the down stage's kernels: O = X W^T (+ residual
+ * when non-null, rounded as above), W [out_features, in_features/2] packed
+ * with scales [out_features, in_features/32] in the checkpoint layout. The
+ * reference computes its dense linears with F.linear
+ * (tinyinfer/layers/linear.py:8-31); this is that call for weights kept in
+ * MXFP4 (qkv_proj, o_proj, lm_head), dequantized exactly in the kernel with
+ * one rounding of the fp32 sum. in_features and out_features must be
+ * multiples of 32; X, W, O (and residual) 16-byte aligned. `path` as in
+ * tinyinfer_mlp_forward_mxfp4_path (TI_PATH_DECODE is refused).
+ */
+int tinyinfer_mxfp4_linear(const void* X, const uint8_t* w, const uint8_t* w_scale, size_t N,
+                           size_t in_features, size_t out_features, const void* residual, void* O,
+                           int dtype_code, int path, void* stream);
+
+/*
  * Device dequantization: out[rows, k] = e2m1(packed) * 2^(scale-127), bit-exact.
  * Replaces dequantize_chunk (tinyinfer/quantization/quantize_mxfp4.py:67-85)
  * and the device decode helpers decode_e2m1 / decode_e8m0

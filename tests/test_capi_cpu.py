@@ -48,7 +48,7 @@ def test_python_constants_match_header(capi):
 
 
 def test_abi_version_and_status_strings(capi):
-    assert capi.lib().tinyinfer_mxfp4_abi_version() == 3
+    assert capi.lib().tinyinfer_mxfp4_abi_version() == 4
     assert capi.status_string(0) == "ok"
     assert "32" in capi.status_string(capi.TI_ERR_BAD_SHAPE)
     assert capi.status_string(999) == "unknown status"
@@ -79,6 +79,17 @@ def test_validation_before_device_work(capi):
     assert dn(p, p, None, 1, 64, 64, p, 1, 0, None) == capi.TI_ERR_INVALID_ARG
     assert dn(p, p, p, 0, 64, 64, p, 1, 0, None) == capi.TI_ERR_INVALID_ARG
     assert dn(p, p, p, 1, 64, 64, p, 1, 4, None) == capi.TI_ERR_INVALID_ARG
+    # residual MLP: null residual, misaligned residual; linear: null X, shapes, misaligned residual
+    rf = L.tinyinfer_mlp_forward_mxfp4_residual
+    assert rf(p, p, p, p, p, p, p, 1, 64, 64, p, None, p, 1, 0, None) == capi.TI_ERR_INVALID_ARG
+    assert rf(p, p, p, p, p, p, p, 1, 64, 64, p, p + 2, p, 1, 0, None) == capi.TI_ERR_MISALIGNED
+    assert rf(p, p, p, p, p, p, p, 1, 64, 64, p, p, p, 1, 9, None) == capi.TI_ERR_INVALID_ARG
+    li = L.tinyinfer_mxfp4_linear
+    assert li(None, p, p, 1, 64, 64, None, p, 1, 0, None) == capi.TI_ERR_INVALID_ARG
+    assert li(p, p, p, 1, 48, 64, None, p, 1, 0, None) == capi.TI_ERR_BAD_SHAPE
+    assert li(p, p, p, 1, 64, 40, None, p, 1, 0, None) == capi.TI_ERR_BAD_SHAPE
+    assert li(p, p, p, 1, 64, 64, p + 8, p, 1, 0, None) == capi.TI_ERR_MISALIGNED
+    assert li(p, p + 1, p, 1, 64, 64, None, p, 1, 0, None) == capi.TI_ERR_MISALIGNED
     assert L.tinyinfer_mxfp4_dequant(p, p, 4, 48, p, 2, None) == capi.TI_ERR_BAD_SHAPE
     assert L.tinyinfer_mxfp4_dequant(p, p, 4, 64, p, 0, None) == capi.TI_ERR_BAD_DTYPE
     assert L.tinyinfer_mxfp4_quantize(p, 2, 4, 64, p, p, None, None) == capi.TI_ERR_INVALID_ARG

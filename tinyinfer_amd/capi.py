@@ -43,6 +43,9 @@ SIGNATURES = {
     "tinyinfer_mlp_forward_mxfp4_path": (_int, [_vp, _u8p, _u8p, _u8p, _u8p, _u8p, _u8p, _sz, _sz, _sz, _vp, _vp, _int, _int, _vp]),
     "tinyinfer_mlp_gate_up_mxfp4": (_int, [_vp, _u8p, _u8p, _u8p, _u8p, _sz, _sz, _sz, _vp, _int, _int, _vp]),
     "tinyinfer_mlp_down_mxfp4": (_int, [_vp, _u8p, _u8p, _sz, _sz, _sz, _vp, _int, _int, _vp]),
+    "tinyinfer_mlp_forward_mxfp4_residual": (_int, [_vp, _u8p, _u8p, _u8p, _u8p, _u8p, _u8p, _sz, _sz, _sz, _vp, _vp,
+                                                    _vp, _int, _int, _vp]),
+    "tinyinfer_mxfp4_linear": (_int, [_vp, _u8p, _u8p, _sz, _sz, _sz, _vp, _vp, _int, _int, _vp]),
     "tinyinfer_mxfp4_dequant": (_int, [_u8p, _u8p, _sz, _sz, _vp, _int, _vp]),
     "tinyinfer_mxfp4_quantize": (_int, [_vp, _int, _sz, _sz, _u8p, _u8p, _vp, _vp]),
     "tinyinfer_mxfp4_diagnostics": (_int, [ctypes.c_void_p]),
@@ -93,11 +96,14 @@ def _act_code(dtype) -> int:
     raise ValueError("MXFP4 MLP only supports FP16 and BF16 activations")
 
 
-def mlp_forward(x, gp, gs, up, us, dp, ds, out=None, tmp=None, path: int = TI_PATH_AUTO, stream=None):
+def mlp_forward(x, gp, gs, up, us, dp, ds, out=None, tmp=None, path: int = TI_PATH_AUTO, stream=None,
+                residual=None):
     """Run the MLP through the C ABI on torch-owned device buffers.
 
     ``out``/``tmp`` may be preallocated ([N, hidden] / [N, intermediate] in
-    ``x``'s dtype); they are allocated when omitted.  Returns ``out``."""
+    ``x``'s dtype); they are allocated when omitted.  With ``residual``
+    ([N, hidden], may be ``out`` itself) the result is ``residual + MLP(x)``,
+    added in the down stage's epilogue.  Returns ``out``."""
     import torch
     n, hidden = x.shape
     inter = gp.shape[0]
@@ -105,10 +111,37 @@ def mlp_forward(x, gp, gs, up, us, dp, ds, out=None, tmp=None, path: int = TI_PA
         out = torch.empty((n, hidden), dtype=x.dtype, device=x.device)
     if tmp is None:
         tmp = torch.empty((n, inter), dtype=x.dtype, device=x.device)
-    st = lib().tinyinfer_mlp_forward_mxfp4_path(
-        x.data_ptr(), gp.data_ptr(), gs.data_ptr(), up.data_ptr(), us.data_ptr(), dp.data_ptr(), ds.data_ptr(),
-        n, hidden, inter, tmp.data_ptr(), out.data_ptr(), _act_code(x.dtype), int(path), _stream_handle(stream))
-    _check(st, "tinyinfer_mlp_forward_mxfp4")
+    if residual is None:
+        st = lib().tinyinfer_mlp_forward_mxfp4_path(
+            x.data_ptr(), gp.data_ptr(), gs.data_ptr(), up.data_ptr(), us.data_ptr(), dp.data_ptr(), ds.data_ptr(),
+            n, hidden, inter, tmp.data_ptr(), out.data_ptr(), _act_code(x.dtype), int(path), _stream_handle(stream))
+        _check(st, "tinyinfer_mlp_forward_mxfp4")
+    else:
+        if tuple(residual.shape) != (n, hidden) or residual.dtype != x.dtype or not residual.is_contiguous():
+            raise ValueError("residual must be a contiguous [N, hidden] tensor of x's dtype")
+        st = lib().tinyinfer_mlp_forward_mxfp4_residual(
+            x.data_ptr(), gp.data_ptr(), gs.data_ptr(), up.data_ptr(), us.data_ptr(), dp.data_ptr(), ds.data_ptr(),
+            n, hidden, inter, tmp.data_ptr(), residual.data_ptr(), out.data_ptr(), _act_code(x.dtype), int(path),
+            _stream_handle(stream))
+        _check(st, "tinyinfer_mlp_forward_mxfp4_residual")
+    return out
+
+
+def linear(x, w, ws, out=None, residual=None, path: int = TI_PATH_AUTO, stream=None):
+    """One MXFP4 linear layer: out = x w^T (+ residual) [N, out_features],
+    w [out_features, in_features/2] packed, ws [out_features, in_features/32]."""
+    import torch
+    n, k = x.shape
+    r = w.shape[0]
+    if out is None:
+        out = torch.empty((n, r), dtype=x.dtype, device=x.device)
+    if residual is not None and (tuple(residual.shape) != (n, r) or residual.dtype != x.dtype
+                                 or not residual.is_contiguous()):
+        raise ValueError("residual must be a contiguous [N, out_features] tensor of x's dtype")
+    st = lib().tinyinfer_mxfp4_linear(
+        x.data_ptr(), w.data_ptr(), ws.data_ptr(), n, k, r, residual.data_ptr() if residual is not None else None,
+        out.data_ptr(), _act_code(x.dtype), int(path), _stream_handle(stream))
+    _check(st, "tinyinfer_mxfp4_linear")
     return out
 
 

@@ -7,7 +7,9 @@
 // per-token kernels, :738) and the N > 32 performance warning (:735-737).
 //
 // Test/bench helpers with no reference counterpart: mlp_forward_mxfp4_path
-// (forced kernel path), mxfp4_dequant, mxfp4_quantize.
+// (forced kernel path), mxfp4_dequant, mxfp4_quantize.  Fusions beyond the
+// reference's call: mlp_forward_mxfp4_residual (the decoder layer's residual
+// add in the down epilogue) and mxfp4_linear (MXFP4 weights for any linear).
 #include <torch/extension.h>
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 #include <c10/core/DeviceGuard.h>
@@ -97,6 +99,62 @@ torch::Tensor mlp_forward_mxfp4_path(torch::Tensor X, torch::Tensor gate, torch:
   return mlp_impl(X, gate, gate_scale, up, up_scale, down, down_scale, (int)path);
 }
 
+// residual + MLP(X), the residual add fused into the down stage
+// (tinyinfer/models/qwen3.py:219 after the MLP call).
+torch::Tensor mlp_forward_mxfp4_residual(torch::Tensor X, torch::Tensor gate, torch::Tensor gate_scale,
+                                         torch::Tensor up, torch::Tensor up_scale, torch::Tensor down,
+                                         torch::Tensor down_scale, torch::Tensor residual) {
+  check_mlp_inputs(X, gate, gate_scale, up, up_scale, down, down_scale);
+  TORCH_CHECK(residual.is_cuda() && residual.device() == X.device(), "X/residual device mismatch");
+  TORCH_CHECK(residual.sizes() == X.sizes() && residual.scalar_type() == X.scalar_type(),
+              "residual must match X's shape and dtype");
+  TORCH_CHECK(residual.is_contiguous(), "residual must be contiguous");
+  const int64_t N = X.size(0), hidden = X.size(1), inter = gate.size(0);
+  const int dtype = X.scalar_type() == at::kHalf ? TI_DTYPE_F16 : TI_DTYPE_BF16;
+  c10::DeviceGuard guard(X.device());
+  auto O = torch::empty({N, hidden}, X.options());
+  auto tmp = torch::empty({N, inter}, X.options());
+  const int st = tinyinfer_mlp_forward_mxfp4_residual(
+      X.data_ptr(), gate.data_ptr<uint8_t>(), gate_scale.data_ptr<uint8_t>(), up.data_ptr<uint8_t>(),
+      up_scale.data_ptr<uint8_t>(), down.data_ptr<uint8_t>(), down_scale.data_ptr<uint8_t>(), (size_t)N,
+      (size_t)hidden, (size_t)inter, tmp.data_ptr(), residual.data_ptr(), O.data_ptr(), dtype, TI_PATH_AUTO,
+      current_stream());
+  check_status(st, "mlp_forward_mxfp4_residual");
+  return O;
+}
+
+// X [N, in] @ dequant(W)^T (+ residual) -> [N, out]; W packed [out, in/2], scales [out, in/32].
+torch::Tensor mxfp4_linear(torch::Tensor X, torch::Tensor w, torch::Tensor w_scale,
+                           c10::optional<torch::Tensor> residual) {
+  TORCH_CHECK(X.is_cuda() && w.is_cuda() && w_scale.is_cuda(), "X/w/w_scale must be CUDA tensors");
+  TORCH_CHECK(X.device() == w.device() && X.device() == w_scale.device(), "X/w device mismatch");
+  TORCH_CHECK(X.dim() == 2 && w.dim() == 2 && w_scale.dim() == 2, "X, w and w_scale must be 2D");
+  TORCH_CHECK(X.scalar_type() == at::kHalf || X.scalar_type() == at::kBFloat16,
+              "MXFP4 linear only supports FP16 and BF16 activations");
+  TORCH_CHECK(w.scalar_type() == at::kByte && w_scale.scalar_type() == at::kByte, "w and w_scale must be uint8");
+  const int64_t N = X.size(0), in = X.size(1), out = w.size(0);
+  TORCH_CHECK(in % 32 == 0 && out % 32 == 0, "in_features and out_features must be divisible by 32");
+  TORCH_CHECK(w.size(1) == in / 2 && w_scale.size(0) == out && w_scale.size(1) == in / 32,
+              "w/w_scale shape mismatch");
+  TORCH_CHECK(X.is_contiguous() && w.is_contiguous() && w_scale.is_contiguous(), "inputs must be contiguous");
+  const void* res = nullptr;
+  if (residual.has_value()) {
+    const auto& r = residual.value();
+    TORCH_CHECK(r.is_cuda() && r.device() == X.device() && r.is_contiguous() && r.dim() == 2 &&
+                    r.size(0) == N && r.size(1) == out && r.scalar_type() == X.scalar_type(),
+                "residual must be a contiguous [N, out_features] tensor of X's dtype on X's device");
+    res = r.data_ptr();
+  }
+  c10::DeviceGuard guard(X.device());
+  auto O = torch::empty({N, out}, X.options());
+  const int st = tinyinfer_mxfp4_linear(X.data_ptr(), w.data_ptr<uint8_t>(), w_scale.data_ptr<uint8_t>(),
+                                        (size_t)N, (size_t)in, (size_t)out, res, O.data_ptr(),
+                                        X.scalar_type() == at::kHalf ? TI_DTYPE_F16 : TI_DTYPE_BF16,
+                                        TI_PATH_AUTO, current_stream());
+  check_status(st, "mxfp4_linear");
+  return O;
+}
+
 // packed [rows, K/2] u8 + scale [rows, K/32] u8 -> [rows, K] float32 or bfloat16.
 torch::Tensor mxfp4_dequant(torch::Tensor packed, torch::Tensor scale, c10::ScalarType out_dtype) {
   TORCH_CHECK(packed.is_cuda() && scale.is_cuda(), "packed/scale must be CUDA tensors");
@@ -157,6 +215,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("mxfp4_dequant", &mxfp4_dequant, "MXFP4 device dequantization", pybind11::arg("packed"),
         pybind11::arg("scale"), pybind11::arg("out_dtype"));
   m.def("mxfp4_quantize", &mxfp4_quantize, "MXFP4 device quantization", pybind11::arg("w"));
+  m.def("mlp_forward_mxfp4_residual", &mlp_forward_mxfp4_residual, "residual + MXFP4 MLP(X)", pybind11::arg("X"),
+        pybind11::arg("gate"), pybind11::arg("gate_scale"), pybind11::arg("up"), pybind11::arg("up_scale"),
+        pybind11::arg("down"), pybind11::arg("down_scale"), pybind11::arg("residual"));
+  m.def("mxfp4_linear", &mxfp4_linear, "MXFP4 linear: X @ dequant(w)^T (+ residual)", pybind11::arg("X"),
+        pybind11::arg("w"), pybind11::arg("w_scale"), pybind11::arg("residual") = pybind11::none());
   m.attr("PATH_AUTO") = TI_PATH_AUTO;
   m.attr("PATH_SKINNY") = TI_PATH_SKINNY;
   m.attr("PATH_GEMM") = TI_PATH_GEMM;

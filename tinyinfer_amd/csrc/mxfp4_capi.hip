@@ -60,6 +60,7 @@ int validate_mlp(const MlpArgs& a, int stage) {
   if ((stage & tinyinfer::kStageGateUp) && (!aligned16(a.x) || !aligned16(a.gate) || !aligned16(a.up)))
     return TI_ERR_MISALIGNED;
   if ((stage & tinyinfer::kStageDown) && !aligned16(a.down)) return TI_ERR_MISALIGNED;
+  if (a.residual && (!(stage & tinyinfer::kStageDown) || !aligned16(a.residual))) return TI_ERR_MISALIGNED;
   return TI_OK;
 }
 
@@ -139,6 +140,28 @@ int tinyinfer_mlp_down_mxfp4(const void* tmp, const uint8_t* down, const uint8_t
   return mlp_impl(a, tinyinfer::kStageDown, path, stream);
 }
 
+int tinyinfer_mlp_forward_mxfp4_residual(const void* X, const uint8_t* gate, const uint8_t* gate_scale,
+                                         const uint8_t* up, const uint8_t* up_scale,
+                                         const uint8_t* down, const uint8_t* down_scale, size_t N,
+                                         size_t hidden_dim, size_t intermediate, void* tmp,
+                                         const void* residual, void* O, int dtype_code, int path,
+                                         void* stream) {
+  if (!residual) return TI_ERR_INVALID_ARG;
+  MlpArgs a{X, gate, gate_scale, up, up_scale, down, down_scale, as_dim(N), as_dim(hidden_dim),
+            as_dim(intermediate), tmp, O, dtype_code, residual};
+  return mlp_impl(a, tinyinfer::kStageBoth, path, stream);
+}
+
+int tinyinfer_mxfp4_linear(const void* X, const uint8_t* w, const uint8_t* w_scale, size_t N,
+                           size_t in_features, size_t out_features, const void* residual, void* O,
+                           int dtype_code, int path, void* stream) {
+  if (!X) return TI_ERR_INVALID_ARG;
+  // the down stage reads its input from tmp: [N, in_features] -> [N, out_features]
+  MlpArgs a{nullptr, nullptr, nullptr, nullptr, nullptr, w, w_scale, as_dim(N), as_dim(out_features),
+            as_dim(in_features), const_cast<void*>(X), O, dtype_code, residual};
+  return mlp_impl(a, tinyinfer::kStageDown, path, stream);
+}
+
 int tinyinfer_mxfp4_dequant(const uint8_t* packed, const uint8_t* scale, size_t rows, size_t k,
                             void* out, int out_dtype, void* stream) {
   if (!packed || !scale || !out) return TI_ERR_INVALID_ARG;
@@ -189,6 +212,6 @@ int tinyinfer_mxfp4_diagnostics(uint32_t* decode_barrier_timeouts) {
   return TI_OK;
 }
 
-int tinyinfer_mxfp4_abi_version(void) { return 3; }
+int tinyinfer_mxfp4_abi_version(void) { return 4; }
 
 }  // extern "C"

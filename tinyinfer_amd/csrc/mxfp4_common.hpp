@@ -128,6 +128,36 @@ __device__ __forceinline__ uint16_t f32_to_act(float f) {
   else return f32_to_f16_rne(f);
 }
 
+template <int DT>
+__device__ __forceinline__ float act_to_f32(uint16_t v) {
+  if constexpr (DT == kBF16) return __uint_as_float((uint32_t)v << 16);
+  else return static_cast<float>(__builtin_bit_cast(_Float16, v));
+}
+
+// A stored down-stage output: the MLP value already rounded to the
+// activation dtype, plus the residual (when there is one) in fp32, rounded
+// again -- what torch computes for `x + mlp(x)` on two activation-dtype
+// tensors (the reference's residual add, tinyinfer/models/qwen3.py:219).
+template <int DT>
+__device__ __forceinline__ uint16_t with_residual(uint16_t v, const uint16_t* res, int64_t idx) {
+  return res ? f32_to_act<DT>(act_to_f32<DT>(res[idx]) + act_to_f32<DT>(v)) : v;
+}
+// The same for four consecutive outputs packed in two dwords (res + idx
+// 8-byte aligned).
+template <int DT>
+__device__ __forceinline__ u32x2_t with_residual4(u32x2_t v, const uint16_t* res, int64_t idx) {
+  if (!res) return v;
+  const u32x2_t r = *reinterpret_cast<const u32x2_t*>(res + idx);
+  u32x2_t o;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const float lo = act_to_f32<DT>((uint16_t)(r[h] & 0xffffu)) + act_to_f32<DT>((uint16_t)(v[h] & 0xffffu));
+    const float hi = act_to_f32<DT>((uint16_t)(r[h] >> 16)) + act_to_f32<DT>((uint16_t)(v[h] >> 16));
+    o[h] = (uint32_t)f32_to_act<DT>(lo) | ((uint32_t)f32_to_act<DT>(hi) << 16);
+  }
+  return o;
+}
+
 // fp16x8 (as 4 dwords) -> exact bf16 hi/lo split: x = hi + lo with both bf16.
 __device__ __forceinline__ void f16x8_split_bf16(u32x4_t v, u32x4_t& hi, u32x4_t& lo) {
   f16x8_t h = __builtin_bit_cast(f16x8_t, v);

@@ -59,6 +59,7 @@ struct GemmPtrs {
   const uint8_t* s[2];     // [N, K/32]
   uint16_t* out;           // [M, N]
   int64_t M, N, K;
+  const uint16_t* res;     // down only: residual [M, N] added to out, or null
 };
 
 // fp16 operand -> exact bf16 hi + lo parts (x = hi + lo)
@@ -248,7 +249,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmPtrs p, int m_til
         }
         lo = (uint32_t)f32_to_act<DT>(v[0]) | ((uint32_t)f32_to_act<DT>(v[1]) << 16);
         hi = (uint32_t)f32_to_act<DT>(v[2]) | ((uint32_t)f32_to_act<DT>(v[3]) << 16);
-        *reinterpret_cast<u32x2_t*>(p.out + tok * N + row) = u32x2_t{lo, hi};
+        *reinterpret_cast<u32x2_t*>(p.out + tok * N + row) = with_residual4<DT>(u32x2_t{lo, hi}, p.res, tok * N + row);
       }
     }
   }
@@ -270,13 +271,13 @@ template <int DT>
 hipError_t run(const MlpArgs& a, int stage, hipStream_t st) {
   if (stage & kStageGateUp) {
     GemmPtrs p{static_cast<const uint16_t*>(a.x), {a.gate, a.up}, {a.gate_scale, a.up_scale},
-               static_cast<uint16_t*>(a.tmp), a.n, a.inter, a.hidden};
+               static_cast<uint16_t*>(a.tmp), a.n, a.inter, a.hidden, nullptr};
     hipError_t e = launch_gemm<DT, 2, 128, 128>(p, st);
     if (e != hipSuccess) return e;
   }
   if (stage & kStageDown) {
     GemmPtrs p{static_cast<const uint16_t*>(a.tmp), {a.down, a.down}, {a.down_scale, a.down_scale},
-               static_cast<uint16_t*>(a.out), a.n, a.hidden, a.inter};
+               static_cast<uint16_t*>(a.out), a.n, a.hidden, a.inter, static_cast<const uint16_t*>(a.residual)};
     return launch_gemm<DT, 1, 128, 128>(p, st);
   }
   return hipSuccess;

@@ -77,6 +77,7 @@ struct RingArgs {
   int m_tiles, n_tiles;
   float* ws;                // split K: fp32 partials [ksplit][M][NMAT * N]
   int ksplit;               // K ranges per tile (1: no split)
+  const uint16_t* res;      // down only: residual [M, N] added to out, or null
 };
 
 // 64 lanes x 16 bytes from per-lane global addresses to 1 KB of LDS at l
@@ -326,7 +327,8 @@ __global__ __launch_bounds__(NW * 64, 2) void gemm_ring_kernel(RingArgs a) {
         }
         const uint32_t lo = (uint32_t)f32_to_act<kBF16>(v[0]) | ((uint32_t)f32_to_act<kBF16>(v[1]) << 16);
         const uint32_t hi = (uint32_t)f32_to_act<kBF16>(v[2]) | ((uint32_t)f32_to_act<kBF16>(v[3]) << 16);
-        *reinterpret_cast<u32x2_t*>(a.out + (int64_t)tok * N + orow) = u32x2_t{lo, hi};
+        const int64_t o = (int64_t)tok * N + orow;
+        *reinterpret_cast<u32x2_t*>(a.out + o) = with_residual4<kBF16>(u32x2_t{lo, hi}, a.res, o);
       }
     }
   }
@@ -335,8 +337,8 @@ __global__ __launch_bounds__(NW * 64, 2) void gemm_ring_kernel(RingArgs a) {
 // out[m][n] = epilogue(sum over ks of ws[ks][m][n] (and [N + n] for up)), in
 // ks order; four outputs per thread.
 template <int NMAT>
-__global__ __launch_bounds__(256) void ring_reduce(const float* __restrict__ ws, uint16_t* __restrict__ out,
-                                                   int M, int N, int ksplit) {
+__global__ __launch_bounds__(256) void ring_reduce(const float* __restrict__ ws, uint16_t* out,
+                                                   const uint16_t* res, int M, int N, int ksplit) {
   const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;   // group of 4 outputs
   const int64_t total = (int64_t)M * N / 4;
   if (q >= total) return;
@@ -353,7 +355,7 @@ __global__ __launch_bounds__(256) void ring_reduce(const float* __restrict__ ws,
   for (int e = 0; e < 4; ++e) v[e] = NMAT == 2 ? silu_f32(g[e]) * u[e] : g[e];
   const uint32_t lo = (uint32_t)f32_to_act<kBF16>(v[0]) | ((uint32_t)f32_to_act<kBF16>(v[1]) << 16);
   const uint32_t hi = (uint32_t)f32_to_act<kBF16>(v[2]) | ((uint32_t)f32_to_act<kBF16>(v[3]) << 16);
-  *reinterpret_cast<u32x2_t*>(out + m * N + n) = u32x2_t{lo, hi};
+  *reinterpret_cast<u32x2_t*>(out + m * N + n) = with_residual4<kBF16>(u32x2_t{lo, hi}, res, m * N + n);
 }
 
 // Split-K workspace: one buffer per (device, stream), grown on demand.  A
@@ -447,7 +449,7 @@ hipError_t launch_ring(RingArgs r, hipStream_t st) {
   const hipError_t e = go(gemm_ring_kernel<NMAT, BM, true, WR, NW>, tiles * ksplit);
   if (e != hipSuccess) return e;
   const int64_t groups = (int64_t)r.M * r.N / 4;
-  ring_reduce<NMAT><<<(unsigned)((groups + 255) / 256), 256, 0, st>>>(r.ws, r.out, r.M, r.N, ksplit);
+  ring_reduce<NMAT><<<(unsigned)((groups + 255) / 256), 256, 0, st>>>(r.ws, r.out, r.res, r.M, r.N, ksplit);
   return hipGetLastError();
 }
 
@@ -486,7 +488,7 @@ bool gemm_ring_supported(const MlpArgs& a, int stage) {
 hipError_t launch_gemm_ring_mlp(const MlpArgs& a, int stage, hipStream_t st) {
   if (stage & kStageGateUp) {
     RingArgs r{static_cast<const uint16_t*>(a.x), {a.gate, a.up}, {a.gate_scale, a.up_scale},
-               static_cast<uint16_t*>(a.tmp), (int)a.n, (int)a.inter, (int)a.hidden, 0, 0, nullptr, 1};
+               static_cast<uint16_t*>(a.tmp), (int)a.n, (int)a.inter, (int)a.hidden, 0, 0, nullptr, 1, nullptr};
     // 256-token tiles once there are enough of them (more reuse of each
     // weight tile), 128 below
     static const int wr = ring_env_wr("TINYINFER_RING_WR_GU");
@@ -499,7 +501,8 @@ hipError_t launch_gemm_ring_mlp(const MlpArgs& a, int stage, hipStream_t st) {
   }
   if (stage & kStageDown) {
     RingArgs r{static_cast<const uint16_t*>(a.tmp), {a.down, a.down}, {a.down_scale, a.down_scale},
-               static_cast<uint16_t*>(a.out), (int)a.n, (int)a.hidden, (int)a.inter, 0, 0, nullptr, 1};
+               static_cast<uint16_t*>(a.out), (int)a.n, (int)a.hidden, (int)a.inter, 0, 0, nullptr, 1,
+               static_cast<const uint16_t*>(a.residual)};
     static const int wr = ring_env_wr("TINYINFER_RING_WR_DN");
     static const int nw = ring_env_nw("TINYINFER_RING_NW_DN");
     if (nw == 4) return wr == 2 ? launch_ring<1, 64, 2, 4>(r, st) : launch_ring<1, 64, 4, 4>(r, st);

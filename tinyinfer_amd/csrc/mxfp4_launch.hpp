@@ -22,6 +22,7 @@ struct MlpArgs {
   void* tmp;                // [n, inter] activation dtype
   void* out;                // [n, hidden] activation dtype
   int dtype;                // kF16 / kBF16
+  const void* residual;     // [n, hidden] or null: out = residual + down(tmp), rounded like torch's add
 };
 
 // Which part of the MLP a launcher runs: the gate_up stage (tmp = SiLU(x G^T) *

@@ -198,7 +198,8 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(const uint16_t* __restr
                                                          const uint8_t* __restrict__ w1,
                                                          const uint8_t* __restrict__ s1, int64_t M,
                                                          int64_t K, int64_t R,
-                                                         uint16_t* __restrict__ out) {
+                                                         uint16_t* out,
+                                                         const uint16_t* res) {   // res may alias out
   constexpr int KS = GATEUP ? NW / 2 : NW;   // K slices
   __shared__ f32x4_t red[NW][T][64];
   __shared__ __attribute__((aligned(16))) uint8_t scale_slices[NW][16 * 4 * NCH];
@@ -243,7 +244,7 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(const uint16_t* __restr
         const int64_t row = row0 + 4 * (lane >> 4) + v;
         if (row < R) {
           const float val = GATEUP ? silu_f32(g[v]) * u[v] : g[v];
-          out[tok * R + row] = f32_to_act<DT>(val);
+          out[tok * R + row] = with_residual<DT>(f32_to_act<DT>(val), res, tok * R + row);
         }
       }
     }
@@ -252,9 +253,10 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(const uint16_t* __restr
 
 template <int DT, int T, int NCH, bool GATEUP, int NW>
 void launch_one(const uint16_t* x, const uint8_t* w0, const uint8_t* s0, const uint8_t* w1,
-                const uint8_t* s1, int64_t M, int64_t K, int64_t R, uint16_t* out, hipStream_t st) {
+                const uint8_t* s1, int64_t M, int64_t K, int64_t R, uint16_t* out, hipStream_t st,
+                const uint16_t* res) {
   dim3 grid((unsigned)((R + 15) / 16), (unsigned)((M + 16 * T - 1) / (16 * T)));
-  skinny_kernel<DT, T, NCH, GATEUP, NW><<<grid, NW * 64, 0, st>>>(x, w0, s0, w1, s1, M, K, R, out);
+  skinny_kernel<DT, T, NCH, GATEUP, NW><<<grid, NW * 64, 0, st>>>(x, w0, s0, w1, s1, M, K, R, out, res);
 }
 
 // Test/tuning override: TINYINFER_SKINNY_NW=<4|8> forces the waves per
@@ -276,7 +278,8 @@ int forced_nw() {
 // tiles x 8 waves x 12 chunks.
 template <int DT, int T, int NCH, bool GATEUP>
 void launch_nw(const uint16_t* x, const uint8_t* w0, const uint8_t* s0, const uint8_t* w1,
-               const uint8_t* s1, int64_t M, int64_t K, int64_t R, uint16_t* out, hipStream_t st) {
+               const uint8_t* s1, int64_t M, int64_t K, int64_t R, uint16_t* out, hipStream_t st,
+               const uint16_t* res) {
   const int64_t tiles = (R + 15) / 16;
   const int64_t chunks = (K + kChunkK - 1) / kChunkK;
   const int64_t mats = GATEUP ? 2 : 1;
@@ -285,21 +288,22 @@ void launch_nw(const uint16_t* x, const uint8_t* w0, const uint8_t* s0, const ui
     const int64_t per_wave4 = (chunks * mats + 3) / 4;
     nw = (per_wave4 <= NCH && tiles * 4 >= 2048) ? 4 : 8;
   }
-  if (nw == 4) launch_one<DT, T, NCH, GATEUP, 4>(x, w0, s0, w1, s1, M, K, R, out, st);
-  else launch_one<DT, T, NCH, GATEUP, 8>(x, w0, s0, w1, s1, M, K, R, out, st);
+  if (nw == 4) launch_one<DT, T, NCH, GATEUP, 4>(x, w0, s0, w1, s1, M, K, R, out, st, res);
+  else launch_one<DT, T, NCH, GATEUP, 8>(x, w0, s0, w1, s1, M, K, R, out, st, res);
 }
 
 // Chunk depth per wave: NCH weight dwordx4 loads in flight per lane; fewer
 // as the per-chunk activation registers (T tiles x 2 x 4 dwordx4) grow.
 template <int DT, bool GATEUP>
 void launch_t(const uint16_t* x, const uint8_t* w0, const uint8_t* s0, const uint8_t* w1,
-              const uint8_t* s1, int64_t M, int64_t K, int64_t R, uint16_t* out, hipStream_t st) {
+              const uint8_t* s1, int64_t M, int64_t K, int64_t R, uint16_t* out, hipStream_t st,
+              const uint16_t* res = nullptr) {
   const int64_t t = M >= 64 ? 4 : (M + 15) / 16;
   switch (t) {
-    case 1: launch_nw<DT, 1, 16, GATEUP>(x, w0, s0, w1, s1, M, K, R, out, st); break;
-    case 2: launch_nw<DT, 2, 8, GATEUP>(x, w0, s0, w1, s1, M, K, R, out, st); break;
-    case 3: launch_nw<DT, 3, 4, GATEUP>(x, w0, s0, w1, s1, M, K, R, out, st); break;
-    default: launch_nw<DT, 4, 4, GATEUP>(x, w0, s0, w1, s1, M, K, R, out, st); break;
+    case 1: launch_nw<DT, 1, 16, GATEUP>(x, w0, s0, w1, s1, M, K, R, out, st, res); break;
+    case 2: launch_nw<DT, 2, 8, GATEUP>(x, w0, s0, w1, s1, M, K, R, out, st, res); break;
+    case 3: launch_nw<DT, 3, 4, GATEUP>(x, w0, s0, w1, s1, M, K, R, out, st, res); break;
+    default: launch_nw<DT, 4, 4, GATEUP>(x, w0, s0, w1, s1, M, K, R, out, st, res); break;
   }
 }
 
@@ -314,7 +318,8 @@ hipError_t run(const MlpArgs& a, int stage, hipStream_t st) {
     if (e != hipSuccess) return e;
   }
   if (stage & kStageDown) {
-    launch_t<DT, false>(h, a.down, a.down_scale, nullptr, nullptr, a.n, a.inter, a.hidden, y, st);
+    launch_t<DT, false>(h, a.down, a.down_scale, nullptr, nullptr, a.n, a.inter, a.hidden, y, st,
+                        static_cast<const uint16_t*>(a.residual));
     return hipGetLastError();
   }
   return hipSuccess;

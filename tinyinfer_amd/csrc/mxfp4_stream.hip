@@ -63,6 +63,7 @@ struct StreamArgs {
   int ss_stride;          // LDS bytes per staged scale row (K/32 + 16: rows fall in different banks)
   int xreg;               // activations in VGPRs (else staged in LDS)
   int lds_scl, lds_red, lds_cnt, lds_out;   // LDS byte offsets
+  const uint16_t* res;    // down only: residual [M, R] added to out, or null
 };
 
 // Wave w's segment run [lo, hi) of a row group (same for both matrices).
@@ -403,7 +404,8 @@ __global__ __launch_bounds__(kNW * 64, 1) void stream_kernel(StreamArgs a) {
   for (int i = threadIdx.x; i < nrg * a.M * 8; i += kThreads) {
     const int li = i / (a.M * 8), rem = i - li * a.M * 8;
     const int t = rem >> 3, r = rem & 7;
-    a.out[(int64_t)t * a.R + (int64_t)(g + li * G) * 8 + r] = outs[i];
+    const int64_t idx = (int64_t)t * a.R + (int64_t)(g + li * G) * 8 + r;
+    a.out[idx] = with_residual<DT>(outs[i], a.res, idx);
   }
 }
 
@@ -536,7 +538,8 @@ hipError_t launch(const StreamArgs& a, int64_t lds, int grid, hipStream_t st) {
 
 template <int DT, bool GATEUP>
 hipError_t run_stage(const uint16_t* x, const uint8_t* w0, const uint8_t* s0, const uint8_t* w1,
-                     const uint8_t* s1, int64_t M, int64_t K, int64_t R, uint16_t* out, hipStream_t st) {
+                     const uint8_t* s1, int64_t M, int64_t K, int64_t R, uint16_t* out, hipStream_t st,
+                     const uint16_t* res = nullptr) {
   StreamArgs a;
   int grid = 0;
   int64_t lds = 0;
@@ -547,6 +550,7 @@ hipError_t run_stage(const uint16_t* x, const uint8_t* w0, const uint8_t* s0, co
   a.w1 = GATEUP ? w1 : w0;
   a.s1 = GATEUP ? s1 : s0;
   a.out = out;
+  a.res = GATEUP ? nullptr : res;
   return launch<DT, GATEUP>(a, lds, grid, st);
 }
 
@@ -900,7 +904,8 @@ __global__ __launch_bounds__(kNW * 64, 1) void fused_kernel(FusedArgs f) {
   for (int i = threadIdx.x; i < nrg2 * B.M * 8; i += kThreads) {
     const int li = i / (B.M * 8), rem = i - li * B.M * 8;
     const int t = rem >> 3, r = rem & 7;
-    B.out[(int64_t)t * B.R + (int64_t)(g + li * G) * 8 + r] = outs2[i];
+    const int64_t idx = (int64_t)t * B.R + (int64_t)(g + li * G) * 8 + r;
+    B.out[idx] = with_residual<DT>(outs2[i], B.res, idx);
   }
 }
 
@@ -950,6 +955,8 @@ hipError_t run_fused(const MlpArgs& m, hipStream_t st) {
   f.d.w0 = f.d.w1 = m.down;
   f.d.s0 = f.d.s1 = m.down_scale;
   f.d.out = static_cast<uint16_t*>(m.out);
+  f.g.res = nullptr;
+  f.d.res = static_cast<const uint16_t*>(m.residual);
   auto go = [&](auto kern) -> hipError_t {
     if (lds > 64 * 1024 &&
         hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -1017,8 +1024,9 @@ hipError_t launch_stream_mlp(const MlpArgs& a, int stage, hipStream_t st) {
     if (e != hipSuccess) return e;
   }
   if (stage & kStageDown) {
-    return bf ? run_stage<kBF16, false>(h, a.down, a.down_scale, nullptr, nullptr, a.n, a.inter, a.hidden, y, st)
-              : run_stage<kF16, false>(h, a.down, a.down_scale, nullptr, nullptr, a.n, a.inter, a.hidden, y, st);
+    const uint16_t* res = static_cast<const uint16_t*>(a.residual);
+    return bf ? run_stage<kBF16, false>(h, a.down, a.down_scale, nullptr, nullptr, a.n, a.inter, a.hidden, y, st, res)
+              : run_stage<kF16, false>(h, a.down, a.down_scale, nullptr, nullptr, a.n, a.inter, a.hidden, y, st, res);
   }
   return hipSuccess;
 }
