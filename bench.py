@@ -283,7 +283,7 @@ def measure_stack(capi, m, reps=5):
             "tok_s": round(m / (ms * 1e-3), 1), "gbs": round(byt / ms / 1e6, 1),
             "hbm_frac": round(byt / ms / 1e6 / HBM_PEAK_GBS, 4), "tflops": round(fl / ms / 1e9, 2),
             "mfma_frac": round(fl / ms / 1e9 / BF16_PEAK_TFLOPS, 4), "reps": reps,
-            "note": "residual adds (torch) included in the time"}
+            "note": "residual add fused into each layer's down epilogue (in place), included in the time"}
 
 
 def main():

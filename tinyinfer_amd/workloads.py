@@ -86,12 +86,17 @@ def activations(m: int, h: int, dtype=torch.bfloat16, seed: int = X_SEED, genera
     return _randn((m, h), seed, generator, None).to(dtype).to(device)
 
 
-def mlp_stack_step(capi, x, layers, out, tmp):
+def mlp_stack_step(capi, x, layers, out, tmp, fused_residual=True):
     """One pass of the Qwen3-32B MLP stack workload: ``x <- x + MLP_l(x)`` for
-    every layer, in the activation dtype (the residual add is torch's, on the
-    current stream, rounding x + out once as the reference's ``x = x + mlp(x)``
-    does).  ``out``/``tmp`` are [M, H] / [M, I] buffers reused by every layer."""
+    every layer, in the activation dtype, rounded as the reference's
+    ``hidden_states = residual + hidden_states``.  With ``fused_residual`` the
+    add happens in the down stage's epilogue, in place on ``x`` (the MLP has
+    read x before down writes it); otherwise it is torch's add of ``out``.
+    ``out``/``tmp`` are [M, H] / [M, I] buffers reused by every layer."""
     for w in layers:
-        capi.mlp_forward(x, *w, out=out, tmp=tmp)
-        x.add_(out)
+        if fused_residual:
+            capi.mlp_forward(x, *w, out=x, tmp=tmp, residual=x)
+        else:
+            capi.mlp_forward(x, *w, out=out, tmp=tmp)
+            x.add_(out)
     return x
