@@ -43,6 +43,7 @@ MALL_BYTES = 256 * 2 ** 20     # Infinity Cache
 PROFILE_DIR = os.path.join(ROOT, "profiles")
 
 METRIC = "MXFP4 MLP GB/s (M=1) & TFLOP/s (M=2048), Qwen3-8B shape, % of peak"
+NORM_EPS = 1e-6                # Qwen3's rms_norm_eps
 
 
 def parse():
@@ -60,7 +61,7 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline sample budget")
     p.add_argument("--copy-probe", action="store_true",
                    help="only run a 256 MiB device copy (calibrates rocprof FETCH/WRITE_SIZE)")
-    p.add_argument("--only", choices=["decode", "gate_up", "down", "prefill"], default=None,
+    p.add_argument("--only", choices=["decode", "gate_up", "down", "prefill", "norm_mlp"], default=None,
                    help="run a single timed loop (for rocprofv3 runs)")
     p.add_argument("--path", type=int, default=0,
                    help="kernel path for --only runs (0 auto, 1 skinny/stream, 2 GEMM, 3 fused decode)")
@@ -93,11 +94,21 @@ class Runner:
         i = sets[0][0].shape[0]
         self.tmp = torch.empty((m, i), dtype=x.dtype, device=x.device)
         self.out = torch.empty((m, h), dtype=x.dtype, device=x.device)
+        if kind in ("norm_mlp", "norm_then_mlp"):
+            g = torch.Generator(device="cpu").manual_seed(17)
+            self.nw = (1.0 + 0.1 * torch.randn(h, generator=g)).to(x.dtype).to(x.device)
+            self.xn = torch.empty((m, h), dtype=x.dtype, device=x.device)
 
     def step(self, s):
         c, w = self.capi, self.sets[s % len(self.sets)]
         if self.kind == "mlp":
             c.mlp_forward(self.x, *w, out=self.out, tmp=self.tmp, path=self.path)
+        elif self.kind == "norm_mlp":          # RMSNorm in the MLP's prologue, residual in its epilogue
+            c.mlp_forward_rmsnorm(self.x, self.nw, NORM_EPS, *w, out=self.out, tmp=self.tmp, xn=self.xn,
+                                  path=self.path)
+        elif self.kind == "norm_then_mlp":     # the same layer half with the norm as its own kernel
+            c.rmsnorm(self.x, self.nw, NORM_EPS, out=self.xn)
+            c.mlp_forward(self.xn, *w, out=self.out, tmp=self.tmp, path=self.path, residual=self.x)
         elif self.kind == "gate_up":
             c.gate_up(self.x, *w[:4], tmp=self.tmp, path=self.path)
         else:
@@ -325,7 +336,8 @@ def main():
     x = activations(m, shape.hidden, device="cuda")
 
     if args.only:
-        kind = {"decode": "mlp", "gate_up": "gate_up", "down": "down", "prefill": "mlp"}[args.only]
+        kind = {"decode": "mlp", "gate_up": "gate_up", "down": "down", "prefill": "mlp",
+                "norm_mlp": "norm_mlp"}[args.only]
         mm = args.prefill_m if args.only == "prefill" else m
         r = Runner(capi, activations(mm, shape.hidden, device="cuda"), sets, kind, path=args.path)
         for s in range(args.warmup):
@@ -375,6 +387,15 @@ def main():
                 "us_per_launch": round(gu_ms * 1e3, 3), "alg_bytes_per_launch": gu_bytes,
                 "down_us_per_launch": round(dn_ms * 1e3, 3)}
 
+    # -- the decoder layer's MLP half: RMSNorm + MLP + residual ----------------
+    # fused (norm in gate_up's prologue, residual in down's epilogue) against
+    # the norm as a kernel of its own in front of the MLP-with-residual
+    nm_ms = statistics.median(Runner(capi, x, sets, "norm_mlp").time_graph(args.steps, reps=3))
+    sep_ms = statistics.median(Runner(capi, x, sets, "norm_then_mlp").time_graph(args.steps, reps=3))
+    decoder_half = {"what": "x + MLP(RMSNorm(x)) per call, M=%d" % m,
+                    "fused_us": round(nm_ms * 1e3, 3), "norm_kernel_then_mlp_us": round(sep_ms * 1e3, 3)}
+    log(f"decoder half: fused {nm_ms * 1e3:.2f} us, norm kernel + MLP {sep_ms * 1e3:.2f} us")
+
     # -- prefill headline -------------------------------------------------------
     prefill = None
     if args.prefill_m:
@@ -415,6 +436,7 @@ def main():
         "wall_ms_timed_region": round(wall_ms, 3),
         "python_call_us": round(py_us, 2),
         "roofline": roofline,
+        "decoder_half": decoder_half,
         "prefill": prefill,
         "cpu_baseline": cpu,
         "points": points or None,

@@ -129,6 +129,39 @@ int tinyinfer_mlp_forward_mxfp4_residual(const void* X, const uint8_t* gate, con
                                          void* stream);
 
 /*
+ * The decoder layer's MLP half with both neighbours fused
+ * (tinyinfer/models/qwen3.py:210-219: residual = hidden; hidden =
+ * post_attention_layernorm(hidden); hidden = mlp(hidden); hidden = residual +
+ * hidden), for a hidden state X [N, hidden]:
+ *   xn = round(norm_weight * X * rsqrt(sum(X^2) / hidden + eps))   per row
+ *   O  = round(X + round(MLP(xn)))
+ * The RMSNorm is the reference's rmsnorm_forward_cuda
+ * (tinyinfer/csrc/rmsnorm.cu:10-54, through layernorm.py:15-23): fp32 inside,
+ * (w * x) * inv in that order. `xn` [N, hidden] receives the normalized rows.
+ * On the streaming decode kernels (N <= 8, AUTO or TI_PATH_SKINNY) the norm
+ * runs in the gate_up kernel's prologue on its LDS copy of X, so the layer
+ * half is two launches; on the other paths a norm kernel writes xn first.
+ * norm_weight [hidden] and xn are in the activation dtype, 16-byte aligned;
+ * O may be X itself (in-place). `path` as in tinyinfer_mlp_forward_mxfp4_path.
+ */
+int tinyinfer_mlp_forward_mxfp4_rmsnorm(const void* X, const void* norm_weight, float eps,
+                                        const uint8_t* gate, const uint8_t* gate_scale, const uint8_t* up,
+                                        const uint8_t* up_scale, const uint8_t* down,
+                                        const uint8_t* down_scale, size_t N, size_t hidden_dim,
+                                        size_t intermediate, void* xn, void* tmp, void* O, int dtype_code,
+                                        int path, void* stream);
+
+/*
+ * RMSNorm alone, the reference's rmsnorm_forward_cuda
+ * (tinyinfer/csrc/rmsnorm.cu:79-123) for fp16 and bf16 rows:
+ * O = round(weight * X * rsqrt(sum(X^2) / hidden + eps)) per row of
+ * `hidden_dim` activations. hidden_dim a multiple of 8; X, weight and O
+ * 16-byte aligned.
+ */
+int tinyinfer_rmsnorm(const void* X, const void* weight, float eps, size_t num_rows, size_t hidden_dim, void* O,
+                      int dtype_code, void* stream);
+
+/*
  * One MXFP4 linear layer on the down stage's kernels: O = X W^T (+ residual
  * when non-null, rounded as above), W [out_features, in_features/2] packed
  * with scales [out_features, in_features/32] in the checkpoint layout. The

@@ -18,6 +18,17 @@ Three forms:
   activation dtype (``mlp_fp4.cu:140``), the down sum is exact and rounded
   once (``mlp_fp4.cu:424``).
 * ``mlp_fp64``: everything in float64, no intermediate rounding.
+
+And the MLP's two neighbours in the decoder layer
+(``tinyinfer/models/qwen3.py:210-219``):
+
+* ``rmsnorm_reference``: the reference's RMSNorm op, ``rmsnorm_forward``
+  (``tinyinfer/layers/layernorm.py:15-23`` -> ``tinyinfer/csrc/rmsnorm.cu:10-54``):
+  per row the sum of squares in fp32, ``inv = rsqrt(sum / hidden + eps)``,
+  ``out = round(w * x * inv)`` evaluated as ``(w * x) * inv`` in fp32.
+* ``decoder_mlp_reference``: ``x + mlp(rmsnorm(x))`` with the sum of the two
+  activation-dtype tensors rounded once, as torch adds them
+  (``qwen3.py:219``).
 """
 
 from __future__ import annotations
@@ -56,6 +67,24 @@ def mlp_reference(x, gp, gs, up, us, dp, ds, weights=None) -> torch.Tensor:
     u = F.linear(xt, wu)
     h = F.silu(g) * u
     return F.linear(h, wd)
+
+
+def rmsnorm_reference(x, w, eps: float) -> torch.Tensor:
+    """The reference's rmsnorm kernel (rmsnorm.cu:10-54) on the CPU, fp32
+    inside, rounded once to x's dtype."""
+    xt = _as_tensor(x).cpu()
+    x32 = xt.to(torch.float32)
+    w32 = _as_tensor(w).cpu().to(torch.float32)
+    ssum = (x32 * x32).sum(dim=-1, keepdim=True)                        # rmsnorm.cu:24-28, fp32
+    inv = torch.rsqrt(ssum / float(xt.shape[-1]) + np.float32(eps))     # rmsnorm.cu:45
+    return ((w32 * x32) * inv).to(xt.dtype)                             # rmsnorm.cu:51-53
+
+
+def decoder_mlp_reference(x, w_norm, eps: float, gp, gs, up, us, dp, ds) -> torch.Tensor:
+    """``x + Qwen3MLP(post_attention_layernorm(x))`` (qwen3.py:210-219)."""
+    xt = _as_tensor(x).cpu()
+    y = mlp_reference(rmsnorm_reference(xt, w_norm, eps), gp, gs, up, us, dp, ds)
+    return (xt.to(torch.float32) + y.to(torch.float32)).to(xt.dtype)
 
 
 def _silu64(v: np.ndarray) -> np.ndarray:

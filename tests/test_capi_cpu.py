@@ -48,7 +48,7 @@ def test_python_constants_match_header(capi):
 
 
 def test_abi_version_and_status_strings(capi):
-    assert capi.lib().tinyinfer_mxfp4_abi_version() == 4
+    assert capi.lib().tinyinfer_mxfp4_abi_version() == 5
     assert capi.status_string(0) == "ok"
     assert "32" in capi.status_string(capi.TI_ERR_BAD_SHAPE)
     assert capi.status_string(999) == "unknown status"
@@ -90,6 +90,18 @@ def test_validation_before_device_work(capi):
     assert li(p, p, p, 1, 64, 40, None, p, 1, 0, None) == capi.TI_ERR_BAD_SHAPE
     assert li(p, p, p, 1, 64, 64, p + 8, p, 1, 0, None) == capi.TI_ERR_MISALIGNED
     assert li(p, p + 1, p, 1, 64, 64, None, p, 1, 0, None) == capi.TI_ERR_MISALIGNED
+    # decoder MLP half with the RMSNorm prologue: null norm weight / xn, misaligned norm weight
+    nf = L.tinyinfer_mlp_forward_mxfp4_rmsnorm
+    assert nf(p, None, 1e-6, p, p, p, p, p, p, 1, 64, 64, p, p, p, 1, 0, None) == capi.TI_ERR_INVALID_ARG
+    assert nf(p, p, 1e-6, p, p, p, p, p, p, 1, 64, 64, None, p, p, 1, 0, None) == capi.TI_ERR_INVALID_ARG
+    assert nf(p, p + 4, 1e-6, p, p, p, p, p, p, 1, 64, 64, p, p, p, 1, 0, None) == capi.TI_ERR_MISALIGNED
+    assert nf(p, p, 1e-6, p, p, p, p, p, p, 1, 48, 64, p, p, p, 1, 0, None) == capi.TI_ERR_BAD_SHAPE
+    assert nf(p, p, 1e-6, p, p, p, p, p, p, 1, 64, 64, p, p, p, 1, 5, None) == capi.TI_ERR_INVALID_ARG
+    rn = L.tinyinfer_rmsnorm
+    assert rn(None, p, 1e-6, 1, 64, p, 1, None) == capi.TI_ERR_INVALID_ARG
+    assert rn(p, p, 1e-6, 1, 60, p, 1, None) == capi.TI_ERR_BAD_SHAPE
+    assert rn(p, p, 1e-6, 1, 64, p, 2, None) == capi.TI_ERR_BAD_DTYPE
+    assert rn(p, p + 2, 1e-6, 1, 64, p, 1, None) == capi.TI_ERR_MISALIGNED
     assert L.tinyinfer_mxfp4_dequant(p, p, 4, 48, p, 2, None) == capi.TI_ERR_BAD_SHAPE
     assert L.tinyinfer_mxfp4_dequant(p, p, 4, 64, p, 0, None) == capi.TI_ERR_BAD_DTYPE
     assert L.tinyinfer_mxfp4_quantize(p, 2, 4, 64, p, p, None, None) == capi.TI_ERR_INVALID_ARG
@@ -121,6 +133,16 @@ def test_torch_wrapper_rejects_host_tensors_with_reference_message():
     assert C.mlp_forward_mxfp4.__doc__.startswith("mlp_forward_mxfp4(X: torch.Tensor, gate: torch.Tensor")
     for n in names:
         assert f"{n}: torch.Tensor" in C.mlp_forward_mxfp4.__doc__
+
+
+def test_rmsnorm_wrappers_reject_host_tensors_with_reference_message():
+    from tinyinfer_amd.extension import load_extension
+    C = load_extension()
+    with pytest.raises(RuntimeError, match="input must be a CUDA tensor"):
+        C.rmsnorm_forward(torch.zeros(2, 64, dtype=torch.bfloat16), torch.ones(64, dtype=torch.bfloat16), 1e-6)
+    args = _cpu_inputs()
+    with pytest.raises(RuntimeError, match="X must be a CUDA tensor"):
+        C.mlp_forward_mxfp4_rmsnorm(args[0], torch.ones(64, dtype=torch.bfloat16), 1e-6, *args[1:])
 
 
 def test_load_extension_is_cached():

@@ -112,3 +112,71 @@ def test_parity_stats_detects_a_transposed_operand():
     assert not om.within_tolerance(om.parity_stats(wrong, ref))
     right = torch.nn.functional.linear(torch.nn.functional.silu(g) * u, wd)
     assert om.within_tolerance(om.parity_stats(right, ref))
+
+
+# ---------------------------------------------------------------- RMSNorm
+# rmsnorm_reference restates tinyinfer/csrc/rmsnorm.cu:10-54.  Pinned by an
+# fp64 brute force (within one bf16 rounding), by torch's own rms_norm
+# routine, by exact power-of-two scale invariance at eps = 0, and by a planted
+# mistake (mean over the wrong length) that the fp64 check must reject.
+
+def _rms_fp64(x, w, eps):
+    x64 = x.to(torch.float64)
+    return w.to(torch.float64) * x64 / torch.sqrt((x64 * x64).mean(-1, keepdim=True) + eps)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_rmsnorm_reference_matches_fp64_within_one_rounding(dtype):
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(5, 256, generator=g).to(dtype)
+    w = (1.0 + 0.1 * torch.randn(256, generator=g)).to(dtype)
+    out = om.rmsnorm_reference(x, w, 1e-6).to(torch.float64)
+    ref = _rms_fp64(x, w, 1e-6)
+    ulp = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10
+    assert float(((out - ref).abs() / ref.abs().clamp_min(1e-30)).max()) <= ulp
+
+
+def test_rmsnorm_reference_matches_torch_rms_norm():
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(7, 512, generator=g).to(torch.bfloat16)
+    w = (1.0 + 0.1 * torch.randn(512, generator=g)).to(torch.bfloat16)
+    lib = torch.nn.functional.rms_norm(x.float(), (512,), w.float(), 1e-6).to(torch.bfloat16)
+    out = om.rmsnorm_reference(x, w, 1e-6)
+    diff = (out.float() - lib.float()).abs()
+    # same math, fp32 summation orders differ: at most one bf16 ulp, almost always equal
+    assert float((diff / lib.float().abs().clamp_min(1e-30)).max()) <= 2.0 ** -7
+    assert float((out == lib).float().mean()) > 0.99
+
+
+def test_rmsnorm_reference_power_of_two_invariance():
+    g = torch.Generator().manual_seed(13)
+    x = torch.randn(3, 128, generator=g).to(torch.bfloat16)
+    w = torch.randn(128, generator=g).to(torch.bfloat16)
+    a = om.rmsnorm_reference(x, w, 0.0)
+    b = om.rmsnorm_reference(x * 8, w, 0.0)       # x and sum scale by 8 and 64: inv by 1/8
+    assert torch.equal(a, b)
+
+
+def test_rmsnorm_planted_mistake_is_caught():
+    g = torch.Generator().manual_seed(14)
+    x = torch.randn(4, 256, generator=g).to(torch.bfloat16)
+    w = torch.ones(256, dtype=torch.bfloat16)
+    x32 = x.float()
+    wrong = (x32 * torch.rsqrt((x32 * x32).sum(-1, keepdim=True) / 255.0 + 1e-6)).to(torch.bfloat16)
+    ref = _rms_fp64(x, w, 1e-6)
+    rel = float(((wrong.to(torch.float64) - ref).abs() / ref.abs().clamp_min(1e-30)).max())
+    assert rel > 2.0 ** -9                        # a length off by one is visible above the rounding
+
+
+def test_decoder_mlp_reference_composition():
+    """x + mlp(rmsnorm(x)): with zero gate weights the MLP is zero and the
+    output is x itself; otherwise it is the two reference ops composed."""
+    x, mats = make_mlp(3, 64, 96, seed=15)
+    w = (1.0 + 0.1 * torch.randn(64, generator=torch.Generator().manual_seed(16))).to(torch.bfloat16)
+    gp, gs, up, us, dp, ds = mats
+    zero = np.zeros_like(gp)
+    same = om.decoder_mlp_reference(x, w, 1e-6, zero, gs, up, us, dp, ds)
+    assert torch.equal(same, x)
+    out = om.decoder_mlp_reference(x, w, 1e-6, *mats)
+    y = om.mlp_reference(om.rmsnorm_reference(x, w, 1e-6), *mats)
+    assert torch.equal(out, (x.float() + y.float()).to(torch.bfloat16))

@@ -45,6 +45,9 @@ SIGNATURES = {
     "tinyinfer_mlp_down_mxfp4": (_int, [_vp, _u8p, _u8p, _sz, _sz, _sz, _vp, _int, _int, _vp]),
     "tinyinfer_mlp_forward_mxfp4_residual": (_int, [_vp, _u8p, _u8p, _u8p, _u8p, _u8p, _u8p, _sz, _sz, _sz, _vp, _vp,
                                                     _vp, _int, _int, _vp]),
+    "tinyinfer_mlp_forward_mxfp4_rmsnorm": (_int, [_vp, _vp, ctypes.c_float, _u8p, _u8p, _u8p, _u8p, _u8p, _u8p,
+                                                   _sz, _sz, _sz, _vp, _vp, _vp, _int, _int, _vp]),
+    "tinyinfer_rmsnorm": (_int, [_vp, _vp, ctypes.c_float, _sz, _sz, _vp, _int, _vp]),
     "tinyinfer_mxfp4_linear": (_int, [_vp, _u8p, _u8p, _sz, _sz, _sz, _vp, _vp, _int, _int, _vp]),
     "tinyinfer_mxfp4_dequant": (_int, [_u8p, _u8p, _sz, _sz, _vp, _int, _vp]),
     "tinyinfer_mxfp4_quantize": (_int, [_vp, _int, _sz, _sz, _u8p, _u8p, _vp, _vp]),
@@ -124,6 +127,44 @@ def mlp_forward(x, gp, gs, up, us, dp, ds, out=None, tmp=None, path: int = TI_PA
             n, hidden, inter, tmp.data_ptr(), residual.data_ptr(), out.data_ptr(), _act_code(x.dtype), int(path),
             _stream_handle(stream))
         _check(st, "tinyinfer_mlp_forward_mxfp4_residual")
+    return out
+
+
+def mlp_forward_rmsnorm(x, norm_w, eps, gp, gs, up, us, dp, ds, out=None, tmp=None, xn=None,
+                        path: int = TI_PATH_AUTO, stream=None):
+    """The decoder layer's MLP half: ``out = x + MLP(RMSNorm(x))`` with the
+    norm in the MLP's prologue.  ``xn`` ([N, hidden], allocated when omitted)
+    receives the normalized rows; ``out`` may be ``x`` itself.  Returns
+    ``(out, xn)``."""
+    import torch
+    n, hidden = x.shape
+    inter = gp.shape[0]
+    if tuple(norm_w.shape) != (hidden,) or norm_w.dtype != x.dtype or not norm_w.is_contiguous():
+        raise ValueError("norm_w must be a contiguous [hidden] tensor of x's dtype")
+    if out is None:
+        out = torch.empty((n, hidden), dtype=x.dtype, device=x.device)
+    if tmp is None:
+        tmp = torch.empty((n, inter), dtype=x.dtype, device=x.device)
+    if xn is None:
+        xn = torch.empty((n, hidden), dtype=x.dtype, device=x.device)
+    st = lib().tinyinfer_mlp_forward_mxfp4_rmsnorm(
+        x.data_ptr(), norm_w.data_ptr(), float(eps), gp.data_ptr(), gs.data_ptr(), up.data_ptr(), us.data_ptr(),
+        dp.data_ptr(), ds.data_ptr(), n, hidden, inter, xn.data_ptr(), tmp.data_ptr(), out.data_ptr(),
+        _act_code(x.dtype), int(path), _stream_handle(stream))
+    _check(st, "tinyinfer_mlp_forward_mxfp4_rmsnorm")
+    return out, xn
+
+
+def rmsnorm(x, w, eps, out=None, stream=None):
+    """RMSNorm of the rows of x ([..., hidden]) with weight w ([hidden])."""
+    import torch
+    hidden = x.shape[-1]
+    rows = x.numel() // hidden
+    if out is None:
+        out = torch.empty_like(x)
+    st = lib().tinyinfer_rmsnorm(x.data_ptr(), w.data_ptr(), float(eps), rows, hidden, out.data_ptr(),
+                                 _act_code(x.dtype), _stream_handle(stream))
+    _check(st, "tinyinfer_rmsnorm")
     return out
 
 

@@ -9,7 +9,9 @@
 // Test/bench helpers with no reference counterpart: mlp_forward_mxfp4_path
 // (forced kernel path), mxfp4_dequant, mxfp4_quantize.  Fusions beyond the
 // reference's call: mlp_forward_mxfp4_residual (the decoder layer's residual
-// add in the down epilogue) and mxfp4_linear (MXFP4 weights for any linear).
+// add in the down epilogue), mlp_forward_mxfp4_rmsnorm (also the
+// post-attention RMSNorm in the prologue) and mxfp4_linear (MXFP4 weights for
+// any linear).  rmsnorm_forward mirrors the reference's op of that name.
 #include <torch/extension.h>
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 #include <c10/core/DeviceGuard.h>
@@ -123,6 +125,60 @@ torch::Tensor mlp_forward_mxfp4_residual(torch::Tensor X, torch::Tensor gate, to
   return O;
 }
 
+// The decoder layer's MLP half (tinyinfer/models/qwen3.py:210-219):
+// X + MLP(RMSNorm(X)), the norm in the MLP's prologue and the residual add in
+// its epilogue.  norm_weight is post_attention_layernorm.weight [hidden].
+torch::Tensor mlp_forward_mxfp4_rmsnorm(torch::Tensor X, torch::Tensor norm_weight, double eps, torch::Tensor gate,
+                                        torch::Tensor gate_scale, torch::Tensor up, torch::Tensor up_scale,
+                                        torch::Tensor down, torch::Tensor down_scale) {
+  check_mlp_inputs(X, gate, gate_scale, up, up_scale, down, down_scale);
+  TORCH_CHECK(norm_weight.is_cuda() && norm_weight.device() == X.device(), "X/norm_weight device mismatch");
+  TORCH_CHECK(norm_weight.dim() == 1 && norm_weight.size(0) == X.size(1),
+              "norm_weight must have shape [hidden_dim]");
+  TORCH_CHECK(norm_weight.scalar_type() == X.scalar_type(), "X/norm_weight dtype mismatch");
+  TORCH_CHECK(norm_weight.is_contiguous(), "norm_weight must be contiguous");
+  const int64_t N = X.size(0), hidden = X.size(1), inter = gate.size(0);
+  const int dtype = X.scalar_type() == at::kHalf ? TI_DTYPE_F16 : TI_DTYPE_BF16;
+  c10::DeviceGuard guard(X.device());
+  auto O = torch::empty({N, hidden}, X.options());
+  auto xn = torch::empty({N, hidden}, X.options());
+  auto tmp = torch::empty({N, inter}, X.options());
+  const int st = tinyinfer_mlp_forward_mxfp4_rmsnorm(
+      X.data_ptr(), norm_weight.data_ptr(), (float)eps, gate.data_ptr<uint8_t>(), gate_scale.data_ptr<uint8_t>(),
+      up.data_ptr<uint8_t>(), up_scale.data_ptr<uint8_t>(), down.data_ptr<uint8_t>(), down_scale.data_ptr<uint8_t>(),
+      (size_t)N, (size_t)hidden, (size_t)inter, xn.data_ptr(), tmp.data_ptr(), O.data_ptr(), dtype, TI_PATH_AUTO,
+      current_stream());
+  check_status(st, "mlp_forward_mxfp4_rmsnorm");
+  return O;
+}
+
+// The reference's rmsnorm_forward (tinyinfer/csrc/bind.cpp:255-293), same
+// name, arguments, checks and messages, for fp16 and bf16 (the reference's
+// fp32 rows are not built here: they raise).
+torch::Tensor rmsnorm_forward(torch::Tensor input, torch::Tensor weight, double eps) {
+  TORCH_CHECK(input.is_cuda(), "input must be a CUDA tensor");
+  TORCH_CHECK(weight.is_cuda(), "weight must be a CUDA tensor");
+  TORCH_CHECK(input.device() == weight.device(), "input/weight must be on the same device");
+  TORCH_CHECK(input.dim() >= 1, "input must have at least 1 dimension");
+  TORCH_CHECK(weight.dim() == 1, "weight must have shape [D]");
+  TORCH_CHECK(input.size(-1) == weight.size(0), "weight size must match input last dimension");
+  TORCH_CHECK(input.scalar_type() == weight.scalar_type(), "input/weight dtype mismatch");
+  TORCH_CHECK(input.is_contiguous(), "input must be contiguous");
+  TORCH_CHECK(weight.is_contiguous(), "weight must be contiguous");
+  TORCH_CHECK(input.scalar_type() == at::kHalf || input.scalar_type() == at::kBFloat16,
+              "RMSNorm supports fp16 and bf16 only");
+  c10::DeviceGuard guard(input.device());
+  auto output = torch::empty_like(input);
+  const int64_t hidden = input.size(-1);
+  const int64_t rows = hidden > 0 ? input.numel() / hidden : 0;
+  if (rows == 0) return output;
+  const int st = tinyinfer_rmsnorm(input.data_ptr(), weight.data_ptr(), (float)eps, (size_t)rows, (size_t)hidden,
+                                   output.data_ptr(), input.scalar_type() == at::kHalf ? TI_DTYPE_F16 : TI_DTYPE_BF16,
+                                   current_stream());
+  check_status(st, "rmsnorm_forward");
+  return output;
+}
+
 // X [N, in] @ dequant(W)^T (+ residual) -> [N, out]; W packed [out, in/2], scales [out, in/32].
 torch::Tensor mxfp4_linear(torch::Tensor X, torch::Tensor w, torch::Tensor w_scale,
                            c10::optional<torch::Tensor> residual) {
@@ -220,6 +276,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         pybind11::arg("down"), pybind11::arg("down_scale"), pybind11::arg("residual"));
   m.def("mxfp4_linear", &mxfp4_linear, "MXFP4 linear: X @ dequant(w)^T (+ residual)", pybind11::arg("X"),
         pybind11::arg("w"), pybind11::arg("w_scale"), pybind11::arg("residual") = pybind11::none());
+  m.def("mlp_forward_mxfp4_rmsnorm", &mlp_forward_mxfp4_rmsnorm, "X + MXFP4 MLP(RMSNorm(X))", pybind11::arg("X"),
+        pybind11::arg("norm_weight"), pybind11::arg("eps"), pybind11::arg("gate"), pybind11::arg("gate_scale"),
+        pybind11::arg("up"), pybind11::arg("up_scale"), pybind11::arg("down"), pybind11::arg("down_scale"));
+  m.def("rmsnorm_forward", &rmsnorm_forward, "RMSNorm forward", pybind11::arg("input"), pybind11::arg("weight"),
+        pybind11::arg("eps"));
   m.attr("PATH_AUTO") = TI_PATH_AUTO;
   m.attr("PATH_SKINNY") = TI_PATH_SKINNY;
   m.attr("PATH_GEMM") = TI_PATH_GEMM;

@@ -152,6 +152,55 @@ int tinyinfer_mlp_forward_mxfp4_residual(const void* X, const uint8_t* gate, con
   return mlp_impl(a, tinyinfer::kStageBoth, path, stream);
 }
 
+int tinyinfer_mlp_forward_mxfp4_rmsnorm(const void* X, const void* norm_weight, float eps,
+                                        const uint8_t* gate, const uint8_t* gate_scale, const uint8_t* up,
+                                        const uint8_t* up_scale, const uint8_t* down,
+                                        const uint8_t* down_scale, size_t N, size_t hidden_dim,
+                                        size_t intermediate, void* xn, void* tmp, void* O, int dtype_code,
+                                        int path, void* stream) {
+  if (!X || !norm_weight || !xn) return TI_ERR_INVALID_ARG;
+  // the hidden state is also the residual
+  MlpArgs a{X, gate, gate_scale, up, up_scale, down, down_scale, as_dim(N), as_dim(hidden_dim),
+            as_dim(intermediate), tmp, O, dtype_code, X};
+  int st = validate_mlp(a, tinyinfer::kStageBoth);
+  if (st != TI_OK) return st;
+  if (!aligned16(norm_weight) || !aligned16(xn)) return TI_ERR_MISALIGNED;
+  if (path != TI_PATH_AUTO && path != TI_PATH_SKINNY && path != TI_PATH_GEMM && path != TI_PATH_DECODE)
+    return TI_ERR_INVALID_ARG;
+  st = check_device();
+  if (st != TI_OK) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // decode sizes on the streaming kernels: the norm in gate_up's prologue
+  const bool small = (size_t)a.n <= kStreamMaxTokens;
+  if (small && (path == TI_PATH_SKINNY || (path == TI_PATH_AUTO && (size_t)a.n < kGemmMinTokens))) {
+    MlpArgs f = a;
+    f.norm_w = norm_weight;
+    f.eps = eps;
+    f.xn = xn;
+    if (tinyinfer::stream_supported(f, tinyinfer::kStageBoth))
+      return to_status(tinyinfer::launch_stream_mlp(f, tinyinfer::kStageBoth, s));
+  }
+  // elsewhere: the norm kernel writes xn, then the MLP on xn with X as residual
+  const hipError_t e = tinyinfer::launch_rmsnorm(X, norm_weight, eps, a.n, a.hidden, xn, dtype_code, s);
+  if (e != hipSuccess) return to_status(e);
+  a.x = xn;
+  return mlp_impl(a, tinyinfer::kStageBoth, path, stream);
+}
+
+int tinyinfer_rmsnorm(const void* X, const void* weight, float eps, size_t num_rows, size_t hidden_dim, void* O,
+                      int dtype_code, void* stream) {
+  if (!X || !weight || !O) return TI_ERR_INVALID_ARG;
+  if (num_rows == 0 || hidden_dim == 0) return TI_ERR_INVALID_ARG;
+  if (hidden_dim % 8 != 0) return TI_ERR_BAD_SHAPE;
+  if (dtype_code != TI_DTYPE_F16 && dtype_code != TI_DTYPE_BF16) return TI_ERR_BAD_DTYPE;
+  if (num_rows > kMaxTokens * 64 || hidden_dim > kMaxDim) return TI_ERR_TOO_LARGE;
+  if (!aligned16(X) || !aligned16(weight) || !aligned16(O)) return TI_ERR_MISALIGNED;
+  const int st = check_device();
+  if (st != TI_OK) return st;
+  return to_status(tinyinfer::launch_rmsnorm(X, weight, eps, (int64_t)num_rows, (int64_t)hidden_dim, O, dtype_code,
+                                             static_cast<hipStream_t>(stream)));
+}
+
 int tinyinfer_mxfp4_linear(const void* X, const uint8_t* w, const uint8_t* w_scale, size_t N,
                            size_t in_features, size_t out_features, const void* residual, void* O,
                            int dtype_code, int path, void* stream) {
@@ -212,6 +261,6 @@ int tinyinfer_mxfp4_diagnostics(uint32_t* decode_barrier_timeouts) {
   return TI_OK;
 }
 
-int tinyinfer_mxfp4_abi_version(void) { return 4; }
+int tinyinfer_mxfp4_abi_version(void) { return 5; }
 
 }  // extern "C"

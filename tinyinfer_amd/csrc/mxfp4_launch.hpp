@@ -23,6 +23,12 @@ struct MlpArgs {
   void* out;                // [n, hidden] activation dtype
   int dtype;                // kF16 / kBF16
   const void* residual;     // [n, hidden] or null: out = residual + down(tmp), rounded like torch's add
+  // RMSNorm prologue (the streaming gate_up kernel only): x is normalized in
+  // the kernel's LDS copy, xn = round(norm_w * x * rsqrt(mean(x^2) + eps)),
+  // and workgroup 0 writes it to xn [n, hidden]; null norm_w: x is used as is
+  const void* norm_w = nullptr;   // [hidden] activation dtype
+  float eps = 0.f;
+  void* xn = nullptr;
 };
 
 // Which part of the MLP a launcher runs: the gate_up stage (tmp = SiLU(x G^T) *
@@ -57,6 +63,13 @@ hipError_t launch_decode_mlp(const MlpArgs& a, hipStream_t stream);
 // Spin timeouts of the fused decode kernel's wait since load (0 unless a
 // workgroup was not resident); synchronous.
 unsigned int decode_barrier_timeouts();
+
+// RMSNorm of n rows of `hidden` activations (the reference's rmsnorm
+// kernel, tinyinfer/csrc/rmsnorm.cu:10-54): out = round(w * x * rsqrt(sum(x^2)
+// / hidden + eps)) per row, fp32 inside.  hidden % 8 == 0, 16-byte aligned
+// rows.
+hipError_t launch_rmsnorm(const void* x, const void* w, float eps, int64_t n, int64_t hidden, void* out,
+                          int dtype, hipStream_t stream);
 
 hipError_t launch_dequant(const uint8_t* packed, const uint8_t* scale, int64_t rows, int64_t k,
                           void* out, int out_dtype, hipStream_t stream);

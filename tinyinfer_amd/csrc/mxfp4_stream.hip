@@ -64,7 +64,17 @@ struct StreamArgs {
   int xreg;               // activations in VGPRs (else staged in LDS)
   int lds_scl, lds_red, lds_cnt, lds_out;   // LDS byte offsets
   const uint16_t* res;    // down only: residual [M, R] added to out, or null
+  const uint16_t* norm_w; // gate_up only: RMSNorm weight [K] applied to x in LDS, or null
+  float eps;
+  uint16_t* xn;           // with norm_w: workgroup 0 writes the normalized x here [M, K]
+  int lds_nw, lds_nsum;   // with norm_w: LDS copy of the weight, partial sums
 };
+
+__device__ __forceinline__ float wave_sum64(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
 
 // Wave w's segment run [lo, hi) of a row group (same for both matrices).
 __device__ __forceinline__ void seg_run(const StreamArgs& a, int wave, int& lo, int& hi) {
@@ -282,6 +292,20 @@ __global__ __launch_bounds__(kNW * 64, 1) void stream_kernel(StreamArgs a) {
   for (int b = 0; b < kXPre; ++b) xv[b] = *x_src(threadIdx.x + b * kThreads);
 #pragma unroll
   for (int b = 0; b < kSPre; ++b) sv[b] = *s_src(threadIdx.x + b * kThreads);
+  // RMSNorm weights (gate_up with a norm): LDS chunk c = elements 8c .. 8c+7,
+  // loaded before the first weights like x
+  const bool norm = GATEUP && a.norm_w != nullptr;
+  const int nwc = a.K / 8;
+  u32x4_t nv[2];
+  if (norm) {
+    for (int c0 = threadIdx.x + 2 * kThreads; c0 < nwc; c0 += kThreads)
+      *reinterpret_cast<u32x4_t*>(lds + a.lds_nw + 16 * c0) = *reinterpret_cast<const u32x4_t*>(a.norm_w + 8 * c0);
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int c = threadIdx.x + b * kThreads;
+      nv[b] = *reinterpret_cast<const u32x4_t*>(a.norm_w + 8 * (c < nwc ? c : nwc - 1));
+    }
+  }
 
   // the first D units in flight (separate named buffers: an array indexed by
   // the pipeline slot ends up in scratch)
@@ -304,13 +328,68 @@ __global__ __launch_bounds__(kNW * 64, 1) void stream_kernel(StreamArgs a) {
 #pragma unroll
   for (int b = 0; b < kSPre; ++b)
     if (threadIdx.x + b * kThreads < nsc) *s_dst(threadIdx.x + b * kThreads) = sv[b];
+  if (norm) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+      if (threadIdx.x + b * kThreads < nwc) *reinterpret_cast<u32x4_t*>(lds + a.lds_nw + 16 * (threadIdx.x + b * kThreads)) = nv[b];
+  }
   // every wave's LDS stores (counters, x, scales) are done before any wave
   // reads them: wait for LDS only (a full __syncthreads would also wait for
   // the weights in flight)
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0xc07f);    // lgkmcnt(0)
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
+  auto lds_barrier = [] {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xc07f);    // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  lds_barrier();
+
+  // RMSNorm of x in LDS while the first weights are in flight (the
+  // reference's post_attention_layernorm, tinyinfer/csrc/rmsnorm.cu:10-54):
+  // per token the sum of squares in fp32 (per thread, over the wave, then
+  // over the waves in order), inv = rsqrt(sum / K + eps), x <- round(w * x *
+  // inv).  Every workgroup normalizes its own copy.
+  if (norm) {
+    float* nsum = reinterpret_cast<float*>(lds + a.lds_nsum);   // [kNW][8] partials, then [8] inverse rms
+    for (int t = 0; t < a.M; ++t) {
+      float sq = 0.f;
+      for (int c = threadIdx.x; c < nwc; c += kThreads) {
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(lds + t * a.xs_stride + 16 * c);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float lo = act_to_f32<DT>((uint16_t)(v[j] & 0xffffu)), hi = act_to_f32<DT>((uint16_t)(v[j] >> 16));
+          sq += lo * lo;
+          sq += hi * hi;
+        }
+      }
+      sq = wave_sum64(sq);
+      if (lane == 0) nsum[wave * 8 + t] = sq;
+    }
+    lds_barrier();
+    if (threadIdx.x < a.M) {
+      float tot = 0.f;
+      for (int w = 0; w < kNW; ++w) tot += nsum[w * 8 + threadIdx.x];
+      nsum[kNW * 8 + threadIdx.x] = rsqrtf(tot / (float)a.K + a.eps);
+    }
+    lds_barrier();
+    for (int t = 0; t < a.M; ++t) {
+      const float inv = nsum[kNW * 8 + t];
+      for (int c = threadIdx.x; c < nwc; c += kThreads) {
+        u32x4_t* xp = reinterpret_cast<u32x4_t*>(lds + t * a.xs_stride + 16 * c);
+        const u32x4_t v = *xp;
+        const u32x4_t gw = *reinterpret_cast<const u32x4_t*>(lds + a.lds_nw + 16 * c);
+        u32x4_t o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float lo = act_to_f32<DT>((uint16_t)(gw[j] & 0xffffu)) * act_to_f32<DT>((uint16_t)(v[j] & 0xffffu)) * inv;
+          const float hi = act_to_f32<DT>((uint16_t)(gw[j] >> 16)) * act_to_f32<DT>((uint16_t)(v[j] >> 16)) * inv;
+          o[j] = (uint32_t)f32_to_act<DT>(lo) | ((uint32_t)f32_to_act<DT>(hi) << 16);
+        }
+        *xp = o;
+      }
+    }
+    lds_barrier();
+  }
 
   // XREG: segment j of the wave's run, MFMA t: x[tok][256 (lo + j) + 32 q8 + 8 t],
   // copied once from LDS; segments past the run read a valid address and are
@@ -407,6 +486,13 @@ __global__ __launch_bounds__(kNW * 64, 1) void stream_kernel(StreamArgs a) {
     const int64_t idx = (int64_t)t * a.R + (int64_t)(g + li * G) * 8 + r;
     a.out[idx] = with_residual<DT>(outs[i], a.res, idx);
   }
+  if (norm && g == 0 && a.xn) {
+    for (int c = threadIdx.x; c < a.M * nwc; c += kThreads) {
+      const int t = c / nwc, cc = c - t * nwc;
+      *reinterpret_cast<u32x4_t*>(a.xn + (int64_t)t * a.K + 8 * cc) =
+          *reinterpret_cast<const u32x4_t*>(lds + t * a.xs_stride + 16 * cc);
+    }
+  }
 }
 
 struct DevCaps {
@@ -478,7 +564,7 @@ bool stream_xreg_allowed(bool gateup) {
 // force_grid > 0 fixes the grid (the fused decode kernel runs both stages on
 // the gate_up stage's grid).
 bool plan(int64_t M, int64_t K, int64_t R, bool gateup, bool bf16, const DevCaps& d, StreamArgs& a, int& grid,
-          int64_t& lds, int force_grid = 0) {
+          int64_t& lds, int force_grid = 0, bool norm = false) {
   // K % 512: a row group's scale rows split into whole 16-byte chunks
   if (d.cus < 1 || M < 1 || M > 8 || K % (2 * kItemK) != 0 || R % 8 != 0) return false;
   if (K > (1 << 20) || R > (1 << 24)) return false;
@@ -503,6 +589,15 @@ bool plan(int64_t M, int64_t K, int64_t R, bool gateup, bool bf16, const DevCaps
   a.lds_cnt = a.lds_red + a.nrg_max * kNW * mats * 64 * 4;
   a.lds_out = a.lds_cnt + 4 * ((a.nrg_max + 3) & ~3);
   lds = a.lds_out + a.nrg_max * (int)M * 8 * 2;
+  a.norm_w = nullptr;
+  a.eps = 0.f;
+  a.xn = nullptr;
+  a.lds_nw = a.lds_nsum = 0;
+  if (norm) {
+    a.lds_nw = (int)((lds + 15) & ~int64_t(15));
+    a.lds_nsum = a.lds_nw + (int)(2 * K);
+    lds = a.lds_nsum + 4 * (kNW * 8 + 8);
+  }
   return lds <= d.max_lds;
 }
 
@@ -539,11 +634,18 @@ hipError_t launch(const StreamArgs& a, int64_t lds, int grid, hipStream_t st) {
 template <int DT, bool GATEUP>
 hipError_t run_stage(const uint16_t* x, const uint8_t* w0, const uint8_t* s0, const uint8_t* w1,
                      const uint8_t* s1, int64_t M, int64_t K, int64_t R, uint16_t* out, hipStream_t st,
-                     const uint16_t* res = nullptr) {
+                     const uint16_t* res = nullptr, const uint16_t* norm_w = nullptr, float eps = 0.f,
+                     uint16_t* xn = nullptr) {
   StreamArgs a;
   int grid = 0;
   int64_t lds = 0;
-  if (!plan(M, K, R, GATEUP, DT == kBF16, caps(), a, grid, lds)) return hipErrorNotSupported;
+  const bool norm = GATEUP && norm_w != nullptr;
+  if (!plan(M, K, R, GATEUP, DT == kBF16, caps(), a, grid, lds, 0, norm)) return hipErrorNotSupported;
+  if (norm) {
+    a.norm_w = norm_w;
+    a.eps = eps;
+    a.xn = xn;
+  }
   a.x = x;
   a.w0 = w0;
   a.s0 = s0;
@@ -1002,7 +1104,9 @@ bool stream_supported(const MlpArgs& a, int stage) {
   int grid = 0;
   int64_t lds = 0;
   const bool bf = a.dtype == kBF16;
-  if ((stage & kStageGateUp) && !plan(a.n, a.hidden, a.inter, true, bf, d, sa, grid, lds)) return false;
+  if ((stage & kStageGateUp) && !plan(a.n, a.hidden, a.inter, true, bf, d, sa, grid, lds, 0, a.norm_w != nullptr))
+    return false;
+  if (a.norm_w && (!aligned16(a.norm_w) || (a.xn && !aligned16(a.xn)))) return false;
   if ((stage & kStageDown) && !plan(a.n, a.inter, a.hidden, false, bf, d, sa, grid, lds)) return false;
   // 16-byte loads of activations, weights and scale rows
   const void* p16[] = {a.x, a.gate, a.up, a.down, a.tmp, a.gate_scale, a.up_scale, a.down_scale};
@@ -1017,10 +1121,12 @@ hipError_t launch_stream_mlp(const MlpArgs& a, int stage, hipStream_t st) {
   uint16_t* y = static_cast<uint16_t*>(a.out);
   const bool bf = a.dtype == kBF16;
   if (stage & kStageGateUp) {
+    const uint16_t* nw = static_cast<const uint16_t*>(a.norm_w);
+    uint16_t* xn = static_cast<uint16_t*>(a.xn);
     const hipError_t e = bf ? run_stage<kBF16, true>(x, a.gate, a.gate_scale, a.up, a.up_scale, a.n, a.hidden,
-                                                     a.inter, h, st)
+                                                     a.inter, h, st, nullptr, nw, a.eps, xn)
                             : run_stage<kF16, true>(x, a.gate, a.gate_scale, a.up, a.up_scale, a.n, a.hidden,
-                                                    a.inter, h, st);
+                                                    a.inter, h, st, nullptr, nw, a.eps, xn);
     if (e != hipSuccess) return e;
   }
   if (stage & kStageDown) {
