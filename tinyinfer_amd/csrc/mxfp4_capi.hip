@@ -90,8 +90,11 @@ int mlp_impl(const MlpArgs& a, int stage, int path, void* stream) {
     if (tinyinfer::gemm_ring_supported(a, stage)) return to_status(tinyinfer::launch_gemm_ring_mlp(a, stage, s));
     return to_status(tinyinfer::launch_gemm_mlp(a, stage, s));
   }
-  // small batches: the streaming kernels where they apply (n <= 8), else the
+  // small batches: the streaming kernels where they apply (one token: the
+  // row-streaming kernels; n <= 8: the 8-row item kernels), else the
   // 16-token-tile skinny kernels
+  if (a.n == 1 && tinyinfer::rowstream_enabled() && tinyinfer::rowstream_supported(a, stage))
+    return to_status(tinyinfer::launch_rowstream_mlp(a, stage, s));
   if ((size_t)a.n <= kStreamMaxTokens && tinyinfer::stream_supported(a, stage))
     return to_status(tinyinfer::launch_stream_mlp(a, stage, s));
   return to_status(tinyinfer::launch_skinny_mlp(a, stage, s));
@@ -177,6 +180,8 @@ int tinyinfer_mlp_forward_mxfp4_rmsnorm(const void* X, const void* norm_weight, 
     f.norm_w = norm_weight;
     f.eps = eps;
     f.xn = xn;
+    if (f.n == 1 && tinyinfer::rowstream_enabled() && tinyinfer::rowstream_supported(f, tinyinfer::kStageBoth))
+      return to_status(tinyinfer::launch_rowstream_mlp(f, tinyinfer::kStageBoth, s));
     if (tinyinfer::stream_supported(f, tinyinfer::kStageBoth))
       return to_status(tinyinfer::launch_stream_mlp(f, tinyinfer::kStageBoth, s));
   }

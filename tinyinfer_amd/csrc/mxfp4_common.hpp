@@ -104,6 +104,27 @@ __device__ __forceinline__ u32x4_t dq8_bf16(uint32_t w, uint32_t b) {
 // True (uniformly across the wave) when every active lane's flag is true.
 __device__ __forceinline__ bool wave_all(bool ok) { return !__any(!ok); }
 
+// Sum over the 64 lanes (all active), the same bits in every lane.  Within
+// each row of 16 lanes by DPP exchanges (xor 1 and xor 2 as quad permutes,
+// then the half-row and row mirrors): a pair's two lanes add the same two
+// values, so they agree; then the four row sums are read into scalars and
+// added in a fixed order.  No LDS round trips (a shuffle is one each).
+template <int kCtrl>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), kCtrl, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float wave_sum64(float v) {
+  v = dpp_add<0xb1>(v);     // quad_perm [1,0,3,2]
+  v = dpp_add<0x4e>(v);     // quad_perm [2,3,0,1]
+  v = dpp_add<0x141>(v);    // row_half_mirror
+  v = dpp_add<0x140>(v);    // row_mirror
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
 // 8 codes -> 8 fp32 (exact, all scale bytes).
 __device__ __forceinline__ void dq8_f32(uint32_t w, uint32_t b, float* out) {
   float s = e8m0_to_f32(b);

@@ -1,0 +1,475 @@
+// Row-streaming MXFP4 GEMV for one token (decode at batch 1): one kernel per
+// MLP stage, the same contract as the M <= 8 stream kernel (mxfp4_stream.hip)
+// for the reference's per-token GEMV kernels mlp_stage1_mxfp4 /
+// mlp_stage2_mxfp4 (tinyinfer/csrc/mlp_fp4.cu:79-142, 365-426).
+//
+// At one token the load pattern decides the speed, so the work is laid out
+// for it (each choice measured on MI355X with a read-only kernel of the same
+// bytes):
+//   * every weight load instruction reads 1 KB of ONE row (lane l: the 16
+//     bytes of 32-element block 64c + l of the row's chunk c).  A load whose
+//     lanes span 8 rows at a 2 KB stride streams about 10% slower;
+//   * a wave owns whole rows (row gw + j * waves of the grid), both matrices
+//     for gate_up, so no partial sums cross waves: no LDS slots, counters or
+//     last-arriver epilogue inside the stream;
+//   * the e8m0 bytes of a chunk are the 64 contiguous bytes of its scale row:
+//     one byte load per lane next to the weight load (one cache line), so
+//     no scale staging and no workgroup barrier wait on scales;
+//   * x (and the RMSNorm weight) are staged once through LDS with one
+//     barrier and copied into VGPRs: lane l keeps the 32 activations of its
+//     own block of every chunk;
+//   * two rows in flight per wave: the loads of row j+2 are issued as soon
+//     as row j has been multiplied.
+//
+// MFMA mapping: with A = the lane's 8 dequantized weights and B = the same
+// lane's 8 activations, the diagonal entry C[i][i] of
+// v_mfma_f32_16x16x32_bf16 sums the products of lanes i, i+16, i+32, i+48;
+// the 16 diagonal entries (lanes 0-3, 20-23, 40-43, 60-63 of the
+// accumulator) added over the wave are the row's dot product.  Four MFMAs
+// per load, as many as the 8-row layout spends.
+#include <algorithm>
+#include <cstdlib>
+#include <type_traits>
+
+#include "mxfp4_common.hpp"
+#include "mxfp4_launch.hpp"
+
+namespace tinyinfer {
+
+namespace {
+
+constexpr int kRW = 8;                 // waves per workgroup
+constexpr int kRThreads = kRW * 64;
+constexpr int kChunkBlocks = 64;       // 32-element blocks per load (1 KB of fp4)
+constexpr int kChunkK = kChunkBlocks * kBlock;
+constexpr int kMaxUC = 6;              // chunks per row (K <= 12288; gate_up K <= 10240)
+
+struct RowArgs {
+  const uint16_t* x;       // [K] activations (x for gate_up, h for down)
+  const uint8_t* w0;       // [R, K/2] gate (or down)
+  const uint8_t* s0;       // [R, K/32]
+  const uint8_t* w1;       // [R, K/2] up (gate_up only; else = w0)
+  const uint8_t* s1;
+  uint16_t* out;           // [R]
+  const uint16_t* res;     // down only: residual [R] added to out, or null
+  const uint16_t* norm_w;  // gate_up only: RMSNorm weight [K], or null
+  float eps;
+  uint16_t* xn;            // with norm_w: workgroup 0 writes the normalized x [K]
+  int K, R;
+  int nc;                  // chunks per row, ceil(K / 2048)
+  int nblk;                // K / 32
+  int full;                // every chunk has all 64 blocks (K % 2048 == 0)
+  int rows_max;            // rows of the busiest wave
+  int lds_nw, lds_sum, lds_out;   // LDS byte offsets
+};
+
+template <int UC, bool GATEUP>
+struct RowBuf {
+  static constexpr int kMats = GATEUP ? 2 : 1;
+  u32x4_t w[kMats * UC];
+  uint32_t s[kMats * UC];   // the aligned dword holding the lane's scale byte (byte lane & 3)
+};
+
+// Loads of one row (clamped to the wave's last row past its end: those
+// repeat addresses already read and are never used).  Scale bytes first, so
+// they have landed whenever the weights they scale have.  Each lane loads the
+// aligned dword that holds its scale byte (K % 128 == 0 keeps scale rows
+// dword-aligned): a byte load's zero-extension is a VALU op the compiler may
+// place right after the issue, where it would wait for the load.
+template <int UC, bool GATEUP>
+__device__ __forceinline__ void issue_row(const RowArgs& a, int64_t row, RowBuf<UC, GATEUP>& b) {
+  constexpr int kMats = GATEUP ? 2 : 1;
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int m = 0; m < kMats; ++m) {
+    const uint8_t* sp = (m ? a.s1 : a.s0) + row * a.nblk;
+#pragma unroll
+    for (int q = 0; q < UC; ++q) {
+      const int c = q < a.nc ? q : a.nc - 1;
+      const int blk = c * kChunkBlocks + lane;
+      b.s[m * UC + q] = *reinterpret_cast<const uint32_t*>(sp + ((blk < a.nblk ? blk : a.nblk - 1) & ~3));
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < kMats; ++m) {
+    const uint8_t* wp = (m ? a.w1 : a.w0) + row * (a.K / 2);
+#pragma unroll
+    for (int q = 0; q < UC; ++q) {
+      const int c = q < a.nc ? q : a.nc - 1;
+      const int blk = c * kChunkBlocks + lane;
+      b.w[m * UC + q] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4_t*>(wp + 16 * (int64_t)(blk < a.nblk ? blk : a.nblk - 1)));
+    }
+  }
+  // rows complete in issue order only if their loads are issued in program
+  // order: keep the scheduler from interleaving two rows' loads
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+__device__ __forceinline__ uint32_t scale_byte(uint32_t dw) {
+  return (dw >> (8 * (threadIdx.x & 3))) & 0xffu;
+}
+
+// The row's dot products (one per matrix) into acc.  FULL: every lane of
+// every chunk holds a real block; otherwise lanes past K multiply a zero
+// weight (scale 1.0) by the zero activation they hold.  FAST: every scale
+// byte in the hardware conversion's exact range.
+template <int DT, int UC, bool GATEUP, bool FAST, bool FULL>
+__device__ __forceinline__ void mma_row(const RowArgs& a, const RowBuf<UC, GATEUP>& b,
+                                        const u32x4_t (&xr)[UC][4], const u32x4_t (&xl)[UC][4],
+                                        f32x4_t (&acc)[2]) {
+  constexpr int kMats = GATEUP ? 2 : 1;
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int m = 0; m < kMats; ++m) {
+#pragma unroll
+    for (int q = 0; q < UC; ++q) {
+      const bool valid = FULL || q * kChunkBlocks + lane < a.nblk;
+      const uint32_t sb = valid ? scale_byte(b.s[m * UC + q]) : 127u;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint32_t wq = valid ? b.w[m * UC + q][t] : 0u;
+        const u32x4_t wa = FAST ? dq8_bf16_fast(wq, sb) : dq8_bf16_exact(wq, sb);
+        if constexpr (DT == kBF16) {
+          acc[m] = mfma16x16x32(wa, xr[q][t], acc[m]);
+        } else {
+          acc[m] = mfma16x16x32(wa, xl[q][t], mfma16x16x32(wa, xr[q][t], acc[m]));
+        }
+      }
+    }
+  }
+}
+
+// fp16 x8 from its exact bf16 hi + lo split (inverse of f16x8_split_bf16).
+__device__ __forceinline__ u32x4_t join_f16x8(const u32x4_t& hi, const u32x4_t& lo) {
+  u32x4_t o;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float a0 = __uint_as_float(hi[j] << 16) + __uint_as_float(lo[j] << 16);
+    const float a1 = __uint_as_float(hi[j] & 0xffff0000u) + __uint_as_float(lo[j] & 0xffff0000u);
+    o[j] = (uint32_t)f32_to_f16_rne(a0) | ((uint32_t)f32_to_f16_rne(a1) << 16);
+  }
+  return o;
+}
+
+// Sum of the diagonal of a 16x16 accumulator (lane l holds C[4(l/16)+v][l%16]).
+__device__ __forceinline__ float diag_sum(const f32x4_t& c) {
+  const int lane = threadIdx.x & 63;
+  const int v = lane & 3;
+  float d = v == 0 ? c[0] : v == 1 ? c[1] : v == 2 ? c[2] : c[3];
+  d = ((lane & 15) >> 2) == (lane >> 4) ? d : 0.f;
+  return wave_sum64(d);
+}
+
+template <int DT, int UC, bool GATEUP>
+__global__ __launch_bounds__(kRThreads, 1) void rowstream_kernel(RowArgs a) {
+  constexpr int kXPre = (UC + 1) / 2;   // 16-byte x chunks per thread: K / 8 <= 256 UC
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int nwaves = gridDim.x * kRW;
+  const int gw = blockIdx.x * kRW + wave;
+  const int rows = gw < a.R ? (a.R - gw + nwaves - 1) / nwaves : 0;
+
+  // Prologue loads, issued before the first weights (loads complete in
+  // issue order): x, and the norm weight when there is one.
+  const int nxc = a.K / 8;
+  const bool norm = GATEUP && a.norm_w != nullptr;
+  u32x4_t xv[kXPre], nv[kXPre];
+#pragma unroll
+  for (int p = 0; p < kXPre; ++p) {
+    const int c = threadIdx.x + p * kRThreads;
+    xv[p] = *reinterpret_cast<const u32x4_t*>(a.x + 8 * (c < nxc ? c : nxc - 1));
+  }
+  if (norm) {
+#pragma unroll
+    for (int p = 0; p < kXPre; ++p) {
+      const int c = threadIdx.x + p * kRThreads;
+      nv[p] = *reinterpret_cast<const u32x4_t*>(a.norm_w + 8 * (c < nxc ? c : nxc - 1));
+    }
+  }
+
+  // the first two rows in flight (separate named buffers: an array indexed
+  // by the pipeline slot would end up in scratch)
+  RowBuf<UC, GATEUP> b0, b1;
+  // (a wave without rows loads a row it does not use: a conditional issue
+  // would make the compiler drain the load queue before the LDS stores)
+  auto row_of = [&](int j) {
+    return rows > 0 ? (int64_t)gw + (int64_t)(j < rows ? j : rows - 1) * nwaves : (int64_t)(gw % a.R);
+  };
+  issue_row<UC, GATEUP>(a, row_of(0), b0);
+  issue_row<UC, GATEUP>(a, row_of(1), b1);
+
+  // x (and the norm weight) into LDS; with a norm, each wave's sum of the
+  // squares of the chunks it loaded (fixed order: per thread, then the wave)
+  float* nsum = reinterpret_cast<float*>(lds + a.lds_sum);
+  float sq = 0.f;
+#pragma unroll
+  for (int p = 0; p < kXPre; ++p) {
+    const int c = threadIdx.x + p * kRThreads;
+    if (c < nxc) {
+      *reinterpret_cast<u32x4_t*>(lds + 16 * c) = xv[p];
+      if (norm) {
+        *reinterpret_cast<u32x4_t*>(lds + a.lds_nw + 16 * c) = nv[p];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float lo = act_to_f32<DT>((uint16_t)(xv[p][j] & 0xffffu));
+          const float hi = act_to_f32<DT>((uint16_t)(xv[p][j] >> 16));
+          sq += lo * lo;
+          sq += hi * hi;
+        }
+      }
+    }
+  }
+  if (norm) {
+    sq = wave_sum64(sq);
+    if (lane == 0) nsum[wave] = sq;
+  }
+  // every wave's LDS stores are done before any wave reads them: wait for
+  // LDS only (a full __syncthreads would also wait for the weights in flight)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);    // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+
+  // the reference's post_attention_layernorm (tinyinfer/csrc/rmsnorm.cu:10-54):
+  // inv = rsqrt(sum / K + eps), the same in every wave and workgroup
+  float inv = 1.f;
+  if (norm) {
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < kRW; ++w) tot += nsum[w];
+    inv = rsqrtf(tot / (float)a.K + a.eps);
+  }
+
+  // lane l's activations: block 64q + l of every chunk q, zero past K; with a
+  // norm, x <- round(w * x * inv).  fp16 is split into exact bf16 hi + lo.
+  u32x4_t xr[UC][4], xl[UC][4];
+#pragma unroll
+  for (int q = 0; q < UC; ++q) {
+    const int blk = q * kChunkBlocks + lane;
+    const bool valid = q < a.nc && blk < a.nblk;
+    const int bc = valid ? blk : 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      u32x4_t v = *reinterpret_cast<const u32x4_t*>(lds + 64 * bc + 16 * t);
+      if (norm) {
+        const u32x4_t g = *reinterpret_cast<const u32x4_t*>(lds + a.lds_nw + 64 * bc + 16 * t);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float lo = act_to_f32<DT>((uint16_t)(g[j] & 0xffffu)) * act_to_f32<DT>((uint16_t)(v[j] & 0xffffu)) * inv;
+          const float hi = act_to_f32<DT>((uint16_t)(g[j] >> 16)) * act_to_f32<DT>((uint16_t)(v[j] >> 16)) * inv;
+          v[j] = (uint32_t)f32_to_act<DT>(lo) | ((uint32_t)f32_to_act<DT>(hi) << 16);
+        }
+      }
+      if (!valid) v = u32x4_t{0u, 0u, 0u, 0u};
+      if constexpr (DT == kBF16) {
+        xr[q][t] = v;
+        xl[q][t] = v;
+      } else {
+        f16x8_split_bf16(v, xr[q][t], xl[q][t]);
+      }
+    }
+  }
+
+  uint16_t* outs = reinterpret_cast<uint16_t*>(lds + a.lds_out);   // [rows_max][kRW]
+  // multiply row j from buffer b; with ISSUE, then load row j + 2 into b
+  auto step = [&](RowBuf<UC, GATEUP>& b, int j, auto issue_tag) {
+    f32x4_t acc[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+    bool ok = true;
+#pragma unroll
+    for (int k = 0; k < RowBuf<UC, GATEUP>::kMats * UC; ++k) ok = ok && e8m0_fast_ok(scale_byte(b.s[k]));
+    if (wave_all(ok)) {
+      if (a.full) mma_row<DT, UC, GATEUP, true, true>(a, b, xr, xl, acc);
+      else mma_row<DT, UC, GATEUP, true, false>(a, b, xr, xl, acc);
+    } else {
+      mma_row<DT, UC, GATEUP, false, false>(a, b, xr, xl, acc);
+    }
+    if constexpr (decltype(issue_tag)::value) issue_row<UC, GATEUP>(a, row_of(j + 2), b);
+    const float y0 = diag_sum(acc[0]);
+    float v = y0;
+    if constexpr (GATEUP) v = silu_f32(y0) * diag_sum(acc[1]);
+    if (lane == 0) outs[j * kRW + wave] = f32_to_act<DT>(v);
+  };
+  constexpr std::true_type kIssue{};
+  constexpr std::false_type kLast{};
+  // Every load issued is a row the wave multiplies: the loop runs while rows
+  // j + 2 and j + 3 exist, and the last two or three rows are peeled off into
+  // straight-line tails.  (Loads past the end would cost their bytes and one
+  // more memory latency before the wave can end; an issue under a condition
+  // inside the loop would make the compiler drain the load queue at every
+  // step.  A wave with one row still loads a second, unused one.)
+  int j = 0;
+  for (; j + 3 < rows; j += 2) {
+    step(b0, j, kIssue);
+    step(b1, j + 1, kIssue);
+  }
+  const int left = rows - j;
+  if (left == 3) {
+    step(b0, j, kIssue);
+    step(b1, j + 1, kLast);
+    step(b0, j + 2, kLast);
+  } else if (left == 2) {
+    step(b0, j, kLast);
+    step(b1, j + 1, kLast);
+  } else if (left == 1) {
+    step(b0, j, kLast);
+  }
+
+  // the rows' outputs, staged in LDS (a global store inside the stream would
+  // make the load-queue accounting path-dependent): 8 consecutive rows per j
+  __syncthreads();
+  for (int i = threadIdx.x; i < a.rows_max * kRW; i += kRThreads) {
+    const int jj = i / kRW, w = i - jj * kRW;
+    const int64_t row = (int64_t)blockIdx.x * kRW + w + (int64_t)jj * nwaves;
+    if (row < a.R) a.out[row] = with_residual<DT>(outs[i], a.res, row);
+  }
+  if (norm && blockIdx.x == 0 && wave == 0 && a.xn) {
+#pragma unroll
+    for (int q = 0; q < UC; ++q) {
+      const int blk = q * kChunkBlocks + lane;
+      if (q < a.nc && blk < a.nblk) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          u32x4_t v = xr[q][t];
+          if constexpr (DT != kBF16) v = join_f16x8(xr[q][t], xl[q][t]);
+          *reinterpret_cast<u32x4_t*>(a.xn + 32 * blk + 8 * t) = v;
+        }
+      }
+    }
+  }
+}
+
+int row_cus() {
+  static int cache[64];
+  static bool init[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (!init[dev]) {
+    hipDeviceProp_t prop;
+    cache[dev] = hipGetDeviceProperties(&prop, dev) == hipSuccess ? prop.multiProcessorCount : 0;
+    init[dev] = true;
+  }
+  return cache[dev];
+}
+
+bool aligned16_ptr(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Chunks per row the kernel is instantiated for (smallest fit).
+int row_uc(int64_t K) {
+  const int64_t nc = (K + kChunkK - 1) / kChunkK;
+  return nc <= kMaxUC ? (int)nc : 0;
+}
+
+bool row_plan(int64_t K, int64_t R, bool gateup, bool norm, int dtype, RowArgs& a, int& grid, int64_t& lds) {
+  const int cus = row_cus();
+  // K % 128: scale rows start dword-aligned
+  if (cus < 1 || K < 128 || K % 128 != 0 || K > (1 << 20) || R < 1 || R > (1 << 24)) return false;
+  const int uc = row_uc(K);
+  if (uc == 0) return false;
+  if (dtype != kBF16 && uc > 3) return false;   // fp16: hi + lo activation registers
+  if (gateup && uc > 5) return false;            // two matrices' loads in flight: VGPRs
+  const int64_t waves_needed = R;
+  grid = (int)std::min<int64_t>(cus, (waves_needed + kRW - 1) / kRW);
+  const int64_t nwaves = (int64_t)grid * kRW;
+  a.K = (int)K;
+  a.R = (int)R;
+  a.nc = (int)((K + kChunkK - 1) / kChunkK);
+  a.nblk = (int)(K / kBlock);
+  a.full = K % kChunkK == 0;
+  a.rows_max = (int)((R + nwaves - 1) / nwaves);
+  int64_t off = K * 2;                       // x
+  a.lds_nw = (int)off;
+  if (gateup && norm) off += K * 2;          // norm weight
+  off = (off + 15) & ~int64_t(15);
+  a.lds_sum = (int)off;
+  off += 4 * kRW;
+  a.lds_out = (int)off;
+  off += 2 * (int64_t)a.rows_max * kRW;
+  lds = (off + 15) & ~int64_t(15);
+  return lds <= 64 * 1024;
+}
+
+template <int DT, int UC, bool GATEUP>
+hipError_t row_launch(const RowArgs& a, int grid, int64_t lds, hipStream_t st) {
+  auto k = rowstream_kernel<DT, UC, GATEUP>;
+  hipLaunchKernelGGL(k, dim3(grid), dim3(kRThreads), (size_t)lds, st, a);
+  return hipGetLastError();
+}
+
+template <int DT, bool GATEUP>
+hipError_t row_dispatch(const RowArgs& a, int grid, int64_t lds, hipStream_t st) {
+  switch (a.nc) {
+    case 1: return row_launch<DT, 1, GATEUP>(a, grid, lds, st);
+    case 2: return row_launch<DT, 2, GATEUP>(a, grid, lds, st);
+    case 3: return row_launch<DT, 3, GATEUP>(a, grid, lds, st);
+    default: break;
+  }
+  if constexpr (DT == kBF16) {
+    switch (a.nc) {
+      case 4: return row_launch<DT, 4, GATEUP>(a, grid, lds, st);
+      case 5: return row_launch<DT, 5, GATEUP>(a, grid, lds, st);
+      default: break;
+    }
+    if constexpr (!GATEUP) {
+      if (a.nc == 6) return row_launch<DT, 6, GATEUP>(a, grid, lds, st);
+    }
+  }
+  return hipErrorNotSupported;
+}
+
+template <bool GATEUP>
+hipError_t row_stage(const MlpArgs& m, hipStream_t st) {
+  RowArgs a;
+  int grid = 0;
+  int64_t lds = 0;
+  const int64_t K = GATEUP ? m.hidden : m.inter;
+  const int64_t R = GATEUP ? m.inter : m.hidden;
+  const bool norm = GATEUP && m.norm_w != nullptr;
+  if (!row_plan(K, R, GATEUP, norm, m.dtype, a, grid, lds)) return hipErrorNotSupported;
+  a.x = static_cast<const uint16_t*>(GATEUP ? m.x : m.tmp);
+  a.w0 = GATEUP ? m.gate : m.down;
+  a.s0 = GATEUP ? m.gate_scale : m.down_scale;
+  a.w1 = GATEUP ? m.up : a.w0;
+  a.s1 = GATEUP ? m.up_scale : a.s0;
+  a.out = static_cast<uint16_t*>(GATEUP ? m.tmp : m.out);
+  a.res = GATEUP ? nullptr : static_cast<const uint16_t*>(m.residual);
+  a.norm_w = norm ? static_cast<const uint16_t*>(m.norm_w) : nullptr;
+  a.eps = m.eps;
+  a.xn = norm ? static_cast<uint16_t*>(m.xn) : nullptr;
+  return m.dtype == kBF16 ? row_dispatch<kBF16, GATEUP>(a, grid, lds, st)
+                          : row_dispatch<kF16, GATEUP>(a, grid, lds, st);
+}
+
+}  // namespace
+
+bool rowstream_enabled() {
+  const char* e = std::getenv("TINYINFER_ROWSTREAM");
+  return !(e && e[0] == '0' && e[1] == '\0');
+}
+
+bool rowstream_supported(const MlpArgs& m, int stage) {
+  if (m.n != 1 || (m.dtype != kBF16 && m.dtype != kF16)) return false;
+  RowArgs a;
+  int grid = 0;
+  int64_t lds = 0;
+  if ((stage & kStageGateUp) && !row_plan(m.hidden, m.inter, true, m.norm_w != nullptr, m.dtype, a, grid, lds))
+    return false;
+  if ((stage & kStageDown) && !row_plan(m.inter, m.hidden, false, false, m.dtype, a, grid, lds)) return false;
+  // 16-byte loads of activations, weights and the norm weight; 16-byte xn stores
+  const void* p16[] = {m.x, m.gate, m.up, m.down, m.tmp, m.norm_w, m.xn};
+  for (const void* p : p16)
+    if (p && !aligned16_ptr(p)) return false;
+  return true;
+}
+
+hipError_t launch_rowstream_mlp(const MlpArgs& m, int stage, hipStream_t st) {
+  if (stage & kStageGateUp) {
+    const hipError_t e = row_stage<true>(m, st);
+    if (e != hipSuccess) return e;
+  }
+  if (stage & kStageDown) return row_stage<false>(m, st);
+  return hipSuccess;
+}
+
+}  // namespace tinyinfer

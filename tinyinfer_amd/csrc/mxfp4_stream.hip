@@ -70,11 +70,6 @@ struct StreamArgs {
   int lds_nw, lds_nsum;   // with norm_w: LDS copy of the weight, partial sums
 };
 
-__device__ __forceinline__ float wave_sum64(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
 
 // Wave w's segment run [lo, hi) of a row group (same for both matrices).
 __device__ __forceinline__ void seg_run(const StreamArgs& a, int wave, int& lo, int& hi) {
