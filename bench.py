@@ -382,7 +382,9 @@ def main():
     workload = f"{shape.name}-m{m}"
     roofline = {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": committed_traffic("gate_up", workload),
-                "kernel": ("gate_up stage: stream_kernel (row-group dequant GEMV on MFMA, SiLU*up epilogue)"
+                "kernel": ("gate_up stage: rowstream_kernel (1 KB single-row loads, MFMA diagonal dot "
+                           "products, SiLU*up epilogue)" if m == 1 else
+                           "gate_up stage: stream_kernel (row-group dequant GEMV on MFMA, SiLU*up epilogue)"
                            if m <= 8 else "gate_up stage: skinny dequant MFMA kernel"),
                 "us_per_launch": round(gu_ms * 1e3, 3), "alg_bytes_per_launch": gu_bytes,
                 "down_us_per_launch": round(dn_ms * 1e3, 3)}
