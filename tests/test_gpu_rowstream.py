@@ -1,6 +1,6 @@
 """GPU parity of the row-streaming kernels (one token, one launch per MLP
 stage): TI_PATH_SKINNY and TI_PATH_AUTO run them for N == 1 when K % 128 == 0
-and the stage's K fits (gate_up K <= 10240, down K <= 12288, fp16 K <= 6144).
+and the stage's K fits (gate_up K <= 8192, down K <= 12288, fp16 K <= 6144).
 
 Each stage is checked against the CPU oracle with the kernel's rounding
 points (exact sums, h rounded once), as for the 8-row stream kernels.  The
@@ -54,7 +54,8 @@ def stages(capi, x, mats, what, cols=None):
     (4096, 12288),   # Qwen3-8B: 2 chunks (gate_up), 6 chunks (down)
     (2560, 9728),    # Qwen3-4B: last chunk 16 of 64 blocks; down 5 chunks, last 48 blocks
     (1152, 5120),    # one partial chunk of 36 blocks; down 2.5 chunks
-    (10240, 1024),   # gate_up at its 5-chunk limit
+    (8192, 1024),    # gate_up at its 4-chunk limit
+    (10240, 1024),   # gate_up beyond it: the 8-row stream kernel; down 1 chunk
     (3072, 128),     # 16 workgroups, one row per wave; down K = 128: a 4-block chunk
     (1024, 32768),   # 16 rows per wave on a 256-CU part
 ])

@@ -57,7 +57,7 @@ hipError_t launch_stream_mlp(const MlpArgs& a, int stage, hipStream_t stream);
 
 // Row-streaming kernels for one token (n == 1): each load reads 1 KB of one
 // weight row, a wave owns whole rows.  rowstream_supported() says whether the
-// call fits (K % 128 == 0; K <= 10240 for gate_up, 12288 for down, fp16 6144;
+// call fits (K % 128 == 0; K <= 8192 for gate_up, 12288 for down, fp16 6144;
 // 16-byte alignment);
 // rowstream_enabled() is false when TINYINFER_ROWSTREAM=0 (then the n <= 8
 // stream kernels serve n == 1).

@@ -42,7 +42,7 @@ constexpr int kRW = 8;                 // waves per workgroup
 constexpr int kRThreads = kRW * 64;
 constexpr int kChunkBlocks = 64;       // 32-element blocks per load (1 KB of fp4)
 constexpr int kChunkK = kChunkBlocks * kBlock;
-constexpr int kMaxUC = 6;              // chunks per row (K <= 12288; gate_up K <= 10240)
+constexpr int kMaxUC = 6;              // chunks per row (K <= 12288; gate_up K <= 8192)
 
 struct RowArgs {
   const uint16_t* x;       // [K] activations (x for gate_up, h for down)
@@ -110,14 +110,17 @@ __device__ __forceinline__ uint32_t scale_byte(uint32_t dw) {
   return (dw >> (8 * (threadIdx.x & 3))) & 0xffu;
 }
 
-// The row's dot products (one per matrix) into acc.  FULL: every lane of
+// The row's dot products (one per matrix) into acc, one accumulator per
+// 8-element slice t: four independent MFMA chains per matrix instead of one
+// (a chain waits out each MFMA's latency; at one token the multiply is
+// otherwise what a wave spends its time on once its rows have landed).  FULL: every lane of
 // every chunk holds a real block; otherwise lanes past K multiply a zero
 // weight (scale 1.0) by the zero activation they hold.  FAST: every scale
 // byte in the hardware conversion's exact range.
 template <int DT, int UC, bool GATEUP, bool FAST, bool FULL>
 __device__ __forceinline__ void mma_row(const RowArgs& a, const RowBuf<UC, GATEUP>& b,
                                         const u32x4_t (&xr)[UC][4], const u32x4_t (&xl)[UC][4],
-                                        f32x4_t (&acc)[2]) {
+                                        f32x4_t (&acc)[2][4]) {
   constexpr int kMats = GATEUP ? 2 : 1;
   const int lane = threadIdx.x & 63;
 #pragma unroll
@@ -131,9 +134,9 @@ __device__ __forceinline__ void mma_row(const RowArgs& a, const RowBuf<UC, GATEU
         const uint32_t wq = valid ? b.w[m * UC + q][t] : 0u;
         const u32x4_t wa = FAST ? dq8_bf16_fast(wq, sb) : dq8_bf16_exact(wq, sb);
         if constexpr (DT == kBF16) {
-          acc[m] = mfma16x16x32(wa, xr[q][t], acc[m]);
+          acc[m][t] = mfma16x16x32(wa, xr[q][t], acc[m][t]);
         } else {
-          acc[m] = mfma16x16x32(wa, xl[q][t], mfma16x16x32(wa, xr[q][t], acc[m]));
+          acc[m][t] = mfma16x16x32(wa, xl[q][t], mfma16x16x32(wa, xr[q][t], acc[m][t]));
         }
       }
     }
@@ -200,6 +203,11 @@ __global__ __launch_bounds__(kRThreads, 1) void rowstream_kernel(RowArgs a) {
   issue_row<UC, GATEUP>(a, row_of(0), b0);
   issue_row<UC, GATEUP>(a, row_of(1), b1);
 
+  // LDS position of 16-byte x chunk c (elements 8c .. 8c+7 = slice c % 4 of
+  // block c / 4): slice-major, so the copy into registers below, where lane l
+  // reads slice t of its block, touches consecutive 16-byte words
+  const int plane = a.K / 2;                 // bytes per slice plane
+  auto xpos = [&](int c) { return (c & 3) * plane + 16 * (c >> 2); };
   // x (and the norm weight) into LDS; with a norm, each wave's sum of the
   // squares of the chunks it loaded (fixed order: per thread, then the wave)
   float* nsum = reinterpret_cast<float*>(lds + a.lds_sum);
@@ -208,9 +216,9 @@ __global__ __launch_bounds__(kRThreads, 1) void rowstream_kernel(RowArgs a) {
   for (int p = 0; p < kXPre; ++p) {
     const int c = threadIdx.x + p * kRThreads;
     if (c < nxc) {
-      *reinterpret_cast<u32x4_t*>(lds + 16 * c) = xv[p];
+      *reinterpret_cast<u32x4_t*>(lds + xpos(c)) = xv[p];
       if (norm) {
-        *reinterpret_cast<u32x4_t*>(lds + a.lds_nw + 16 * c) = nv[p];
+        *reinterpret_cast<u32x4_t*>(lds + a.lds_nw + xpos(c)) = nv[p];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const float lo = act_to_f32<DT>((uint16_t)(xv[p][j] & 0xffffu));
@@ -252,9 +260,9 @@ __global__ __launch_bounds__(kRThreads, 1) void rowstream_kernel(RowArgs a) {
     const int bc = valid ? blk : 0;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      u32x4_t v = *reinterpret_cast<const u32x4_t*>(lds + 64 * bc + 16 * t);
+      u32x4_t v = *reinterpret_cast<const u32x4_t*>(lds + xpos(4 * bc + t));
       if (norm) {
-        const u32x4_t g = *reinterpret_cast<const u32x4_t*>(lds + a.lds_nw + 64 * bc + 16 * t);
+        const u32x4_t g = *reinterpret_cast<const u32x4_t*>(lds + a.lds_nw + xpos(4 * bc + t));
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const float lo = act_to_f32<DT>((uint16_t)(g[j] & 0xffffu)) * act_to_f32<DT>((uint16_t)(v[j] & 0xffffu)) * inv;
@@ -275,7 +283,11 @@ __global__ __launch_bounds__(kRThreads, 1) void rowstream_kernel(RowArgs a) {
   uint16_t* outs = reinterpret_cast<uint16_t*>(lds + a.lds_out);   // [rows_max][kRW]
   // multiply row j from buffer b; with ISSUE, then load row j + 2 into b
   auto step = [&](RowBuf<UC, GATEUP>& b, int j, auto issue_tag) {
-    f32x4_t acc[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+    f32x4_t acc[2][4];
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[m][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     bool ok = true;
 #pragma unroll
     for (int k = 0; k < RowBuf<UC, GATEUP>::kMats * UC; ++k) ok = ok && e8m0_fast_ok(scale_byte(b.s[k]));
@@ -286,9 +298,9 @@ __global__ __launch_bounds__(kRThreads, 1) void rowstream_kernel(RowArgs a) {
       mma_row<DT, UC, GATEUP, false, false>(a, b, xr, xl, acc);
     }
     if constexpr (decltype(issue_tag)::value) issue_row<UC, GATEUP>(a, row_of(j + 2), b);
-    const float y0 = diag_sum(acc[0]);
+    const float y0 = diag_sum((acc[0][0] + acc[0][1]) + (acc[0][2] + acc[0][3]));
     float v = y0;
-    if constexpr (GATEUP) v = silu_f32(y0) * diag_sum(acc[1]);
+    if constexpr (GATEUP) v = silu_f32(y0) * diag_sum((acc[1][0] + acc[1][1]) + (acc[1][2] + acc[1][3]));
     if (lane == 0) outs[j * kRW + wave] = f32_to_act<DT>(v);
   };
   constexpr std::true_type kIssue{};
@@ -368,7 +380,7 @@ bool row_plan(int64_t K, int64_t R, bool gateup, bool norm, int dtype, RowArgs& 
   const int uc = row_uc(K);
   if (uc == 0) return false;
   if (dtype != kBF16 && uc > 3) return false;   // fp16: hi + lo activation registers
-  if (gateup && uc > 5) return false;            // two matrices' loads in flight: VGPRs
+  if (gateup && uc > 4) return false;            // two matrices' loads in flight: VGPRs
   const int64_t waves_needed = R;
   grid = (int)std::min<int64_t>(cus, (waves_needed + kRW - 1) / kRW);
   const int64_t nwaves = (int64_t)grid * kRW;
@@ -406,12 +418,9 @@ hipError_t row_dispatch(const RowArgs& a, int grid, int64_t lds, hipStream_t st)
     default: break;
   }
   if constexpr (DT == kBF16) {
-    switch (a.nc) {
-      case 4: return row_launch<DT, 4, GATEUP>(a, grid, lds, st);
-      case 5: return row_launch<DT, 5, GATEUP>(a, grid, lds, st);
-      default: break;
-    }
+    if (a.nc == 4) return row_launch<DT, 4, GATEUP>(a, grid, lds, st);
     if constexpr (!GATEUP) {
+      if (a.nc == 5) return row_launch<DT, 5, GATEUP>(a, grid, lds, st);
       if (a.nc == 6) return row_launch<DT, 6, GATEUP>(a, grid, lds, st);
     }
   }
