@@ -70,6 +70,19 @@ constexpr size_t kGemmMinTokens = 96;
 // Token count up to which the streaming decode kernels are used.
 constexpr size_t kStreamMaxTokens = 8;
 
+// One stage of a small batch on the best kernel that takes it: one token on
+// the row-streaming kernels, n <= 8 on the 8-row item kernels, else the
+// 16-token-tile skinny kernels.  Chosen per stage: the two stages' K differ
+// (at 8B and n = 8 down's activations exceed the LDS the item kernel stages
+// them in, while gate_up's fit).
+hipError_t small_stage(const MlpArgs& a, int st, hipStream_t s) {
+  if (a.n == 1 && tinyinfer::rowstream_enabled() && tinyinfer::rowstream_supported(a, st))
+    return tinyinfer::launch_rowstream_mlp(a, st, s);
+  if ((size_t)a.n <= kStreamMaxTokens && tinyinfer::stream_supported(a, st))
+    return tinyinfer::launch_stream_mlp(a, st, s);
+  return tinyinfer::launch_skinny_mlp(a, st, s);
+}
+
 int mlp_impl(const MlpArgs& a, int stage, int path, void* stream) {
   // sizes arrive as size_t; anything that wraps negative is rejected here
   int st = validate_mlp(a, stage);
@@ -90,14 +103,12 @@ int mlp_impl(const MlpArgs& a, int stage, int path, void* stream) {
     if (tinyinfer::gemm_ring_supported(a, stage)) return to_status(tinyinfer::launch_gemm_ring_mlp(a, stage, s));
     return to_status(tinyinfer::launch_gemm_mlp(a, stage, s));
   }
-  // small batches: the streaming kernels where they apply (one token: the
-  // row-streaming kernels; n <= 8: the 8-row item kernels), else the
-  // 16-token-tile skinny kernels
-  if (a.n == 1 && tinyinfer::rowstream_enabled() && tinyinfer::rowstream_supported(a, stage))
-    return to_status(tinyinfer::launch_rowstream_mlp(a, stage, s));
-  if ((size_t)a.n <= kStreamMaxTokens && tinyinfer::stream_supported(a, stage))
-    return to_status(tinyinfer::launch_stream_mlp(a, stage, s));
-  return to_status(tinyinfer::launch_skinny_mlp(a, stage, s));
+  if (stage & tinyinfer::kStageGateUp) {
+    const hipError_t e = small_stage(a, tinyinfer::kStageGateUp, s);
+    if (e != hipSuccess) return to_status(e);
+  }
+  if (stage & tinyinfer::kStageDown) return to_status(small_stage(a, tinyinfer::kStageDown, s));
+  return TI_OK;
 }
 
 int64_t as_dim(size_t v) { return v > (size_t)INT64_MAX ? -1 : (int64_t)v; }
@@ -180,10 +191,15 @@ int tinyinfer_mlp_forward_mxfp4_rmsnorm(const void* X, const void* norm_weight, 
     f.norm_w = norm_weight;
     f.eps = eps;
     f.xn = xn;
-    if (f.n == 1 && tinyinfer::rowstream_enabled() && tinyinfer::rowstream_supported(f, tinyinfer::kStageBoth))
-      return to_status(tinyinfer::launch_rowstream_mlp(f, tinyinfer::kStageBoth, s));
-    if (tinyinfer::stream_supported(f, tinyinfer::kStageBoth))
-      return to_status(tinyinfer::launch_stream_mlp(f, tinyinfer::kStageBoth, s));
+    hipError_t e = hipErrorNotSupported;
+    if (f.n == 1 && tinyinfer::rowstream_enabled() && tinyinfer::rowstream_supported(f, tinyinfer::kStageGateUp))
+      e = tinyinfer::launch_rowstream_mlp(f, tinyinfer::kStageGateUp, s);
+    else if (tinyinfer::stream_supported(f, tinyinfer::kStageGateUp))
+      e = tinyinfer::launch_stream_mlp(f, tinyinfer::kStageGateUp, s);
+    if (e != hipErrorNotSupported) {
+      if (e != hipSuccess) return to_status(e);
+      return to_status(small_stage(a, tinyinfer::kStageDown, s));   // residual = X
+    }
   }
   // elsewhere: the norm kernel writes xn, then the MLP on xn with X as residual
   const hipError_t e = tinyinfer::launch_rmsnorm(X, norm_weight, eps, a.n, a.hidden, xn, dtype_code, s);

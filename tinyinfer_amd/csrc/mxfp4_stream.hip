@@ -449,26 +449,50 @@ __global__ __launch_bounds__(kNW * 64, 1) void stream_kernel(StreamArgs a) {
       compute_unit<DT, SPU, GATEUP>(a, wave, rgi, part, b.w, scl, xf, acc);
     }
   };
-  auto step = [&](Buf& b, int u) {
+  // multiply unit u from buffer b; with ISSUE, then load unit u + D into b
+  auto step = [&](Buf& b, int u, auto issue_tag) {
     const int rgi = u / P, part = u - rgi * P;
     if (part == 0) acc[0] = acc[1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     compute(b, rgi, part);
-    issue(b, u + D);
+    if constexpr (decltype(issue_tag)::value) issue(b, u + D);
     if (part == P - 1) finish_rg(rgi, acc);
   };
+  constexpr std::true_type kIssue{};
+  constexpr std::false_type kLast{};
   // One exit, at the top: a break between the steps would join the loop's
   // back edge with a path on which the buffers were issued in another order,
   // and the compiler's load-queue bookkeeping would then wait for all of them
   // at the top of every iteration.
   int u = 0;
-  for (; u + D - 1 < units; u += D) {
-    step(b0, u);
-    step(b1, u + 1);
-    if constexpr (D > 2) step(b2, u + 2);
-  }
-  if (u < units) step(b0, u);
-  if constexpr (D > 2) {
-    if (u + 1 < units) step(b1, u + 1);
+  if constexpr (D == 2) {
+    // every load issued is a unit the wave multiplies: the loop runs while
+    // units u + 2 and u + 3 exist and the last two or three units are peeled
+    // into straight-line tails (loads past the end cost their bytes and one
+    // more memory latency before the wave can end; an issue under a condition
+    // inside the loop would drain the load queue at every step)
+    for (; u + 3 < units; u += 2) {
+      step(b0, u, kIssue);
+      step(b1, u + 1, kIssue);
+    }
+    const int left = units - u;
+    if (left == 3) {
+      step(b0, u, kIssue);
+      step(b1, u + 1, kLast);
+      step(b0, u + 2, kLast);
+    } else if (left == 2) {
+      step(b0, u, kLast);
+      step(b1, u + 1, kLast);
+    } else if (left == 1) {
+      step(b0, u, kLast);
+    }
+  } else {
+    for (; u + D - 1 < units; u += D) {
+      step(b0, u, kIssue);
+      step(b1, u + 1, kIssue);
+      step(b2, u + 2, kIssue);
+    }
+    if (u < units) step(b0, u, kIssue);
+    if (u + 1 < units) step(b1, u + 1, kIssue);
   }
 
   // the row groups' outputs, staged in LDS by their last waves (a global
