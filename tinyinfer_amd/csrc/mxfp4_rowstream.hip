@@ -166,7 +166,7 @@ __device__ __forceinline__ float diag_sum(const f32x4_t& c) {
 
 template <int DT, int UC, bool GATEUP>
 __global__ __launch_bounds__(kRThreads, 1) void rowstream_kernel(RowArgs a) {
-  constexpr int kXPre = (UC + 1) / 2;   // 16-byte x chunks per thread: K / 8 <= 256 UC
+  constexpr int kXPre = (256 * UC + kRThreads - 1) / kRThreads;   // 16-byte x chunks per thread: K / 8 <= 256 UC
   extern __shared__ __align__(16) uint8_t lds[];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
