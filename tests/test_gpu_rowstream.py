@@ -58,6 +58,8 @@ def stages(capi, x, mats, what, cols=None):
     (10240, 1024),   # gate_up beyond it: the 8-row stream kernel; down 1 chunk
     (3072, 128),     # 16 workgroups, one row per wave; down K = 128: a 4-block chunk
     (1024, 32768),   # 16 rows per wave on a 256-CU part
+    (1024, 16384),   # down K = 16384: two waves per row, 4 chunks each
+    (5120, 25600),   # Qwen3-32B: gate_up 2.5 chunks; down 12.5 chunks over four waves (3, 3, 3, 4)
 ])
 def test_rowstream_stage_shapes(capi, h, i):
     banner(f"rowstream stages h={h} i={i}")
@@ -94,7 +96,7 @@ def test_rowstream_scale_bytes_outside_fast_range(capi):
     assert torch.isnan(y[0, 1500]) and torch.isfinite(y[0, rest]).all()
 
 
-@pytest.mark.parametrize("h,i", [(1024, 3072), (2560, 6144), (6144, 2048)])
+@pytest.mark.parametrize("h,i", [(1024, 3072), (2560, 6144), (6144, 2048), (1024, 8192)])
 def test_rowstream_fp16(capi, h, i):
     banner(f"rowstream fp16 h={h} i={i}")
     x, mats = make_case(1, h, i, seed=31 + h, dtype=torch.float16)
@@ -169,3 +171,23 @@ def test_rowstream_matches_item_stream_kernels(capi):
     assert sum("rowstream_kernel" in n for n in names["1"]) == 2, names["1"]
     assert not any("rowstream_kernel" in n for n in names["0"]), names["0"]
     assert sum("stream_kernel<" in n for n in names["0"]) == 2, names["0"]
+
+
+@pytest.mark.parametrize("split", ["1", "2", "4"])
+def test_rowstream_down_split_override(capi, split):
+    """TINYINFER_ROW_SPLIT_DOWN picks how many waves share a down row (the
+    8B down stage has 6 chunks: 6, 3 + 3 or 1 + 2 + 1 + 2); every choice
+    agrees with the oracle and sums its parts in a fixed order."""
+    banner(f"rowstream down split {split}")
+    x, mats = make_case(1, 4096, 12288, seed=321)
+    xd, md = to_dev(x, mats)
+    os.environ["TINYINFER_ROW_SPLIT_DOWN"] = split
+    try:
+        h = capi.gate_up(xd, *md[:4], path=SKINNY)
+        out = capi.down(h, *md[4:], path=SKINNY)
+        again = capi.down(h, *md[4:], path=SKINNY)
+        torch.cuda.synchronize()
+    finally:
+        del os.environ["TINYINFER_ROW_SPLIT_DOWN"]
+    assert torch.equal(out.view(torch.int16), again.view(torch.int16))
+    check_close(out.cpu(), down_semantics(h.cpu(), mats[4], mats[5]), f"split {split}")

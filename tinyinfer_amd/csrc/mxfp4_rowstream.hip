@@ -42,7 +42,7 @@ constexpr int kRW = 8;                 // waves per workgroup
 constexpr int kRThreads = kRW * 64;
 constexpr int kChunkBlocks = 64;       // 32-element blocks per load (1 KB of fp4)
 constexpr int kChunkK = kChunkBlocks * kBlock;
-constexpr int kMaxUC = 6;              // chunks per row (K <= 12288; gate_up K <= 8192)
+constexpr int kMaxUC = 6;              // chunks per wave (down; gate_up 4, fp16 3)
 
 struct RowArgs {
   const uint16_t* x;       // [K] activations (x for gate_up, h for down)
@@ -77,7 +77,7 @@ struct RowBuf {
 // dword-aligned): a byte load's zero-extension is a VALU op the compiler may
 // place right after the issue, where it would wait for the load.
 template <int UC, bool GATEUP>
-__device__ __forceinline__ void issue_row(const RowArgs& a, int64_t row, RowBuf<UC, GATEUP>& b) {
+__device__ __forceinline__ void issue_row(const RowArgs& a, int64_t row, int cb, int ncs, RowBuf<UC, GATEUP>& b) {
   constexpr int kMats = GATEUP ? 2 : 1;
   const int lane = threadIdx.x & 63;
 #pragma unroll
@@ -85,7 +85,7 @@ __device__ __forceinline__ void issue_row(const RowArgs& a, int64_t row, RowBuf<
     const uint8_t* sp = (m ? a.s1 : a.s0) + row * a.nblk;
 #pragma unroll
     for (int q = 0; q < UC; ++q) {
-      const int c = q < a.nc ? q : a.nc - 1;
+      const int c = cb + (q < ncs ? q : ncs - 1);
       const int blk = c * kChunkBlocks + lane;
       b.s[m * UC + q] = *reinterpret_cast<const uint32_t*>(sp + ((blk < a.nblk ? blk : a.nblk - 1) & ~3));
     }
@@ -95,7 +95,7 @@ __device__ __forceinline__ void issue_row(const RowArgs& a, int64_t row, RowBuf<
     const uint8_t* wp = (m ? a.w1 : a.w0) + row * (a.K / 2);
 #pragma unroll
     for (int q = 0; q < UC; ++q) {
-      const int c = q < a.nc ? q : a.nc - 1;
+      const int c = cb + (q < ncs ? q : ncs - 1);
       const int blk = c * kChunkBlocks + lane;
       b.w[m * UC + q] = __builtin_nontemporal_load(
           reinterpret_cast<const u32x4_t*>(wp + 16 * (int64_t)(blk < a.nblk ? blk : a.nblk - 1)));
@@ -110,15 +110,17 @@ __device__ __forceinline__ uint32_t scale_byte(uint32_t dw) {
   return (dw >> (8 * (threadIdx.x & 3))) & 0xffu;
 }
 
-// The row's dot products (one per matrix) into acc, one accumulator per
+// The row's dot products (one per matrix) over chunks [cb, cb + ncs) into
+// acc, one accumulator per
 // 8-element slice t: four independent MFMA chains per matrix instead of one
 // (a chain waits out each MFMA's latency; at one token the multiply is
 // otherwise what a wave spends its time on once its rows have landed).  FULL: every lane of
-// every chunk holds a real block; otherwise lanes past K multiply a zero
+// every slot holds a real block; otherwise slots past the range (they hold a
+// repeat of its last chunk) and lanes past K multiply a zero
 // weight (scale 1.0) by the zero activation they hold.  FAST: every scale
 // byte in the hardware conversion's exact range.
 template <int DT, int UC, bool GATEUP, bool FAST, bool FULL>
-__device__ __forceinline__ void mma_row(const RowArgs& a, const RowBuf<UC, GATEUP>& b,
+__device__ __forceinline__ void mma_row(const RowArgs& a, int cb, int ncs, const RowBuf<UC, GATEUP>& b,
                                         const u32x4_t (&xr)[UC][4], const u32x4_t (&xl)[UC][4],
                                         f32x4_t (&acc)[2][4]) {
   constexpr int kMats = GATEUP ? 2 : 1;
@@ -127,7 +129,7 @@ __device__ __forceinline__ void mma_row(const RowArgs& a, const RowBuf<UC, GATEU
   for (int m = 0; m < kMats; ++m) {
 #pragma unroll
     for (int q = 0; q < UC; ++q) {
-      const bool valid = FULL || q * kChunkBlocks + lane < a.nblk;
+      const bool valid = FULL || (q < ncs && (cb + q) * kChunkBlocks + lane < a.nblk);
       const uint32_t sb = valid ? scale_byte(b.s[m * UC + q]) : 127u;
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
@@ -164,15 +166,23 @@ __device__ __forceinline__ float diag_sum(const f32x4_t& c) {
   return wave_sum64(d);
 }
 
-template <int DT, int UC, bool GATEUP>
+// S waves share each row (S divides the workgroup's 8 waves): wave s of the
+// group multiplies chunks [s nc / S, (s + 1) nc / S) and the S partial sums
+// are added in order at the end.  UC is the largest share.
+template <int DT, int UC, bool GATEUP, int S>
 __global__ __launch_bounds__(kRThreads, 1) void rowstream_kernel(RowArgs a) {
-  constexpr int kXPre = (256 * UC + kRThreads - 1) / kRThreads;   // 16-byte x chunks per thread: K / 8 <= 256 UC
+  static_assert(kRW % S == 0, "the waves sharing a row are in one workgroup");
+  // 16-byte x chunks per thread: K / 8 <= 256 UC S (x is staged whole)
+  constexpr int kXPre = (256 * UC * S + kRThreads - 1) / kRThreads;
   extern __shared__ __align__(16) uint8_t lds[];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  const int nwaves = gridDim.x * kRW;
-  const int gw = blockIdx.x * kRW + wave;
-  const int rows = gw < a.R ? (a.R - gw + nwaves - 1) / nwaves : 0;
+  const int nslots = gridDim.x * (kRW / S);
+  const int slot = blockIdx.x * (kRW / S) + wave / S;   // row slot: rows slot + j * nslots
+  const int sp = wave % S;                               // this wave's part of the row
+  const int cb = sp * a.nc / S;
+  const int ncs = (sp + 1) * a.nc / S - cb;
+  const int rows = slot < a.R ? (a.R - slot + nslots - 1) / nslots : 0;
 
   // Prologue loads, issued before the first weights (loads complete in
   // issue order): x, and the norm weight when there is one.
@@ -198,10 +208,10 @@ __global__ __launch_bounds__(kRThreads, 1) void rowstream_kernel(RowArgs a) {
   // (a wave without rows loads a row it does not use: a conditional issue
   // would make the compiler drain the load queue before the LDS stores)
   auto row_of = [&](int j) {
-    return rows > 0 ? (int64_t)gw + (int64_t)(j < rows ? j : rows - 1) * nwaves : (int64_t)(gw % a.R);
+    return rows > 0 ? (int64_t)slot + (int64_t)(j < rows ? j : rows - 1) * nslots : (int64_t)(slot % a.R);
   };
-  issue_row<UC, GATEUP>(a, row_of(0), b0);
-  issue_row<UC, GATEUP>(a, row_of(1), b1);
+  issue_row<UC, GATEUP>(a, row_of(0), cb, ncs, b0);
+  issue_row<UC, GATEUP>(a, row_of(1), cb, ncs, b1);
 
   // LDS position of 16-byte x chunk c (elements 8c .. 8c+7 = slice c % 4 of
   // block c / 4): slice-major, so the copy into registers below, where lane l
@@ -250,13 +260,14 @@ __global__ __launch_bounds__(kRThreads, 1) void rowstream_kernel(RowArgs a) {
     inv = rsqrtf(tot / (float)a.K + a.eps);
   }
 
-  // lane l's activations: block 64q + l of every chunk q, zero past K; with a
-  // norm, x <- round(w * x * inv).  fp16 is split into exact bf16 hi + lo.
+  // lane l's activations: block 64c + l of each of its chunks c = cb + q,
+  // zero past K; with a norm, x <- round(w * x * inv).  fp16 is split into
+  // exact bf16 hi + lo.
   u32x4_t xr[UC][4], xl[UC][4];
 #pragma unroll
   for (int q = 0; q < UC; ++q) {
-    const int blk = q * kChunkBlocks + lane;
-    const bool valid = q < a.nc && blk < a.nblk;
+    const int blk = (cb + q) * kChunkBlocks + lane;
+    const bool valid = q < ncs && blk < a.nblk;
     const int bc = valid ? blk : 0;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -280,7 +291,7 @@ __global__ __launch_bounds__(kRThreads, 1) void rowstream_kernel(RowArgs a) {
     }
   }
 
-  uint16_t* outs = reinterpret_cast<uint16_t*>(lds + a.lds_out);   // [rows_max][kRW]
+  float* outs = reinterpret_cast<float*>(lds + a.lds_out);   // [rows_max][kRW][2] partial sums
   // multiply row j from buffer b; with ISSUE, then load row j + 2 into b
   auto step = [&](RowBuf<UC, GATEUP>& b, int j, auto issue_tag) {
     f32x4_t acc[2][4];
@@ -292,16 +303,16 @@ __global__ __launch_bounds__(kRThreads, 1) void rowstream_kernel(RowArgs a) {
 #pragma unroll
     for (int k = 0; k < RowBuf<UC, GATEUP>::kMats * UC; ++k) ok = ok && e8m0_fast_ok(scale_byte(b.s[k]));
     if (wave_all(ok)) {
-      if (a.full) mma_row<DT, UC, GATEUP, true, true>(a, b, xr, xl, acc);
-      else mma_row<DT, UC, GATEUP, true, false>(a, b, xr, xl, acc);
+      if (a.full && ncs == UC) mma_row<DT, UC, GATEUP, true, true>(a, cb, ncs, b, xr, xl, acc);
+      else mma_row<DT, UC, GATEUP, true, false>(a, cb, ncs, b, xr, xl, acc);
     } else {
-      mma_row<DT, UC, GATEUP, false, false>(a, b, xr, xl, acc);
+      mma_row<DT, UC, GATEUP, false, false>(a, cb, ncs, b, xr, xl, acc);
     }
-    if constexpr (decltype(issue_tag)::value) issue_row<UC, GATEUP>(a, row_of(j + 2), b);
+    if constexpr (decltype(issue_tag)::value) issue_row<UC, GATEUP>(a, row_of(j + 2), cb, ncs, b);
     const float y0 = diag_sum((acc[0][0] + acc[0][1]) + (acc[0][2] + acc[0][3]));
-    float v = y0;
-    if constexpr (GATEUP) v = silu_f32(y0) * diag_sum((acc[1][0] + acc[1][1]) + (acc[1][2] + acc[1][3]));
-    if (lane == 0) outs[j * kRW + wave] = f32_to_act<DT>(v);
+    float y1 = 0.f;
+    if constexpr (GATEUP) y1 = diag_sum((acc[1][0] + acc[1][1]) + (acc[1][2] + acc[1][3]));
+    if (lane == 0) *reinterpret_cast<f32x2_t*>(outs + 2 * (j * kRW + wave)) = f32x2_t{y0, y1};
   };
   constexpr std::true_type kIssue{};
   constexpr std::false_type kLast{};
@@ -328,19 +339,30 @@ __global__ __launch_bounds__(kRThreads, 1) void rowstream_kernel(RowArgs a) {
     step(b0, j, kLast);
   }
 
-  // the rows' outputs, staged in LDS (a global store inside the stream would
-  // make the load-queue accounting path-dependent): 8 consecutive rows per j
+  // the rows' partial sums, staged in LDS (a global store inside the stream
+  // would make the load-queue accounting path-dependent): the S parts of a
+  // row added in order, then the epilogue; 8 / S consecutive rows per j
   __syncthreads();
-  for (int i = threadIdx.x; i < a.rows_max * kRW; i += kRThreads) {
-    const int jj = i / kRW, w = i - jj * kRW;
-    const int64_t row = (int64_t)blockIdx.x * kRW + w + (int64_t)jj * nwaves;
-    if (row < a.R) a.out[row] = with_residual<DT>(outs[i], a.res, row);
+  for (int i = threadIdx.x; i < a.rows_max * (kRW / S); i += kRThreads) {
+    const int jj = i / (kRW / S), sl = i - jj * (kRW / S);
+    const int64_t row = (int64_t)blockIdx.x * (kRW / S) + sl + (int64_t)jj * nslots;
+    if (row < a.R) {
+      float y0 = 0.f, y1 = 0.f;
+#pragma unroll
+      for (int p = 0; p < S; ++p) {
+        const f32x2_t v = *reinterpret_cast<const f32x2_t*>(outs + 2 * (jj * kRW + sl * S + p));
+        y0 += v[0];
+        y1 += v[1];
+      }
+      const float v = GATEUP ? silu_f32(y0) * y1 : y0;
+      a.out[row] = with_residual<DT>(f32_to_act<DT>(v), a.res, row);
+    }
   }
-  if (norm && blockIdx.x == 0 && wave == 0 && a.xn) {
+  if (norm && blockIdx.x == 0 && wave < S && a.xn) {
 #pragma unroll
     for (int q = 0; q < UC; ++q) {
-      const int blk = q * kChunkBlocks + lane;
-      if (q < a.nc && blk < a.nblk) {
+      const int blk = (cb + q) * kChunkBlocks + lane;
+      if (q < ncs && blk < a.nblk) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           u32x4_t v = xr[q][t];
@@ -367,29 +389,46 @@ int row_cus() {
 
 bool aligned16_ptr(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Chunks per row the kernel is instantiated for (smallest fit).
-int row_uc(int64_t K) {
-  const int64_t nc = (K + kChunkK - 1) / kChunkK;
-  return nc <= kMaxUC ? (int)nc : 0;
+int split_env(const char* name) {
+  const char* e = std::getenv(name);
+  const int v = e ? std::atoi(e) : 0;
+  return v == 1 || v == 2 || v == 4 ? v : 0;
 }
 
-bool row_plan(int64_t K, int64_t R, bool gateup, bool norm, int dtype, RowArgs& a, int& grid, int64_t& lds) {
+// Waves per row S and chunks per wave UC for a stage: S in {1, 2, 4} (gate_up
+// 1, 2) so that the largest share fits the VGPR budget (gate_up 4 chunks: two
+// matrices in flight; down 6; fp16 3, its activations are held as hi + lo)
+// and, for down, holds at most 3 chunks where possible; or the S that
+// TINYINFER_ROW_SPLIT_GATEUP / _DOWN names, if that fits.
+bool row_plan(int64_t K, int64_t R, bool gateup, bool norm, int dtype, RowArgs& a, int& grid, int64_t& lds,
+              int& S, int& uc) {
   const int cus = row_cus();
   // K % 128: scale rows start dword-aligned
   if (cus < 1 || K < 128 || K % 128 != 0 || K > (1 << 20) || R < 1 || R > (1 << 24)) return false;
-  const int uc = row_uc(K);
-  if (uc == 0) return false;
-  if (dtype != kBF16 && uc > 3) return false;   // fp16: hi + lo activation registers
-  if (gateup && uc > 4) return false;            // two matrices' loads in flight: VGPRs
-  const int64_t waves_needed = R;
-  grid = (int)std::min<int64_t>(cus, (waves_needed + kRW - 1) / kRW);
-  const int64_t nwaves = (int64_t)grid * kRW;
+  const int nc = (int)((K + kChunkK - 1) / kChunkK);
+  const int ucmax = dtype != kBF16 ? 3 : gateup ? 4 : kMaxUC;
+  const int smax = gateup ? 2 : 4;
+  S = 0;
+  const int want = split_env(gateup ? "TINYINFER_ROW_SPLIT_GATEUP" : "TINYINFER_ROW_SPLIT_DOWN");
+  if (want && want <= smax && (nc + want - 1) / want <= ucmax && want <= nc) S = want;
+  // down: at most 3 chunks per wave where the split allows it (8B down, 6
+  // chunks: 3 + 3 measured 6.36 us against 7.38 us whole and 7.22 us over four
+  // waves); gate_up: whole rows (3 + 3 split measured no faster)
+  const int ucpref = gateup ? ucmax : 3;
+  for (int s = 1; S == 0 && s <= smax; s *= 2)
+    if ((nc + s - 1) / s <= ucpref) S = s;
+  for (int s = 1; S == 0 && s <= smax; s *= 2)
+    if ((nc + s - 1) / s <= ucmax) S = s;
+  if (S == 0 || S > nc) return false;
+  uc = (nc + S - 1) / S;
+  grid = (int)std::min<int64_t>(cus, (R * S + kRW - 1) / kRW);
+  const int64_t nslots = (int64_t)grid * (kRW / S);
   a.K = (int)K;
   a.R = (int)R;
-  a.nc = (int)((K + kChunkK - 1) / kChunkK);
+  a.nc = nc;
   a.nblk = (int)(K / kBlock);
   a.full = K % kChunkK == 0;
-  a.rows_max = (int)((R + nwaves - 1) / nwaves);
+  a.rows_max = (int)((R + nslots - 1) / nslots);
   int64_t off = K * 2;                       // x
   a.lds_nw = (int)off;
   if (gateup && norm) off += K * 2;          // norm weight
@@ -397,32 +436,45 @@ bool row_plan(int64_t K, int64_t R, bool gateup, bool norm, int dtype, RowArgs& 
   a.lds_sum = (int)off;
   off += 4 * kRW;
   a.lds_out = (int)off;
-  off += 2 * (int64_t)a.rows_max * kRW;
+  off += 8 * (int64_t)a.rows_max * kRW;      // two fp32 partial sums per (row, wave)
   lds = (off + 15) & ~int64_t(15);
-  return lds <= 64 * 1024;
+  return lds <= 160 * 1024;
 }
 
-template <int DT, int UC, bool GATEUP>
+template <int DT, int UC, bool GATEUP, int S>
 hipError_t row_launch(const RowArgs& a, int grid, int64_t lds, hipStream_t st) {
-  auto k = rowstream_kernel<DT, UC, GATEUP>;
+  auto k = rowstream_kernel<DT, UC, GATEUP, S>;
+  if (lds > 64 * 1024 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+          hipSuccess)
+    return hipErrorNotSupported;
   hipLaunchKernelGGL(k, dim3(grid), dim3(kRThreads), (size_t)lds, st, a);
   return hipGetLastError();
 }
 
-template <int DT, bool GATEUP>
-hipError_t row_dispatch(const RowArgs& a, int grid, int64_t lds, hipStream_t st) {
-  switch (a.nc) {
-    case 1: return row_launch<DT, 1, GATEUP>(a, grid, lds, st);
-    case 2: return row_launch<DT, 2, GATEUP>(a, grid, lds, st);
-    case 3: return row_launch<DT, 3, GATEUP>(a, grid, lds, st);
+// The instantiated (UC, S) pairs: gate_up S = 1, UC <= 4; down S = 1, 2, 4
+// with UC <= 6 (fp16: UC <= 3).
+template <int DT, bool GATEUP, int S>
+hipError_t row_dispatch_s(const RowArgs& a, int uc, int grid, int64_t lds, hipStream_t st) {
+  constexpr int kMax = DT != kBF16 ? 3 : GATEUP ? 4 : kMaxUC;
+  switch (uc) {
+    case 1: if constexpr (S == 1 || GATEUP) return row_launch<DT, 1, GATEUP, S>(a, grid, lds, st); break;
+    case 2: return row_launch<DT, 2, GATEUP, S>(a, grid, lds, st);
+    case 3: return row_launch<DT, 3, GATEUP, S>(a, grid, lds, st);
+    case 4: if constexpr (kMax >= 4) return row_launch<DT, 4, GATEUP, S>(a, grid, lds, st); break;
+    case 5: if constexpr (kMax >= 5) return row_launch<DT, 5, GATEUP, S>(a, grid, lds, st); break;
+    case 6: if constexpr (kMax >= 6) return row_launch<DT, 6, GATEUP, S>(a, grid, lds, st); break;
     default: break;
   }
-  if constexpr (DT == kBF16) {
-    if (a.nc == 4) return row_launch<DT, 4, GATEUP>(a, grid, lds, st);
-    if constexpr (!GATEUP) {
-      if (a.nc == 5) return row_launch<DT, 5, GATEUP>(a, grid, lds, st);
-      if (a.nc == 6) return row_launch<DT, 6, GATEUP>(a, grid, lds, st);
-    }
+  return hipErrorNotSupported;
+}
+
+template <int DT, bool GATEUP>
+hipError_t row_dispatch(const RowArgs& a, int S, int uc, int grid, int64_t lds, hipStream_t st) {
+  if (S == 1) return row_dispatch_s<DT, GATEUP, 1>(a, uc, grid, lds, st);
+  if (S == 2) return row_dispatch_s<DT, GATEUP, 2>(a, uc, grid, lds, st);
+  if constexpr (!GATEUP) {
+    if (S == 4) return row_dispatch_s<DT, GATEUP, 4>(a, uc, grid, lds, st);
   }
   return hipErrorNotSupported;
 }
@@ -435,7 +487,8 @@ hipError_t row_stage(const MlpArgs& m, hipStream_t st) {
   const int64_t K = GATEUP ? m.hidden : m.inter;
   const int64_t R = GATEUP ? m.inter : m.hidden;
   const bool norm = GATEUP && m.norm_w != nullptr;
-  if (!row_plan(K, R, GATEUP, norm, m.dtype, a, grid, lds)) return hipErrorNotSupported;
+  int S = 0, uc = 0;
+  if (!row_plan(K, R, GATEUP, norm, m.dtype, a, grid, lds, S, uc)) return hipErrorNotSupported;
   a.x = static_cast<const uint16_t*>(GATEUP ? m.x : m.tmp);
   a.w0 = GATEUP ? m.gate : m.down;
   a.s0 = GATEUP ? m.gate_scale : m.down_scale;
@@ -446,8 +499,8 @@ hipError_t row_stage(const MlpArgs& m, hipStream_t st) {
   a.norm_w = norm ? static_cast<const uint16_t*>(m.norm_w) : nullptr;
   a.eps = m.eps;
   a.xn = norm ? static_cast<uint16_t*>(m.xn) : nullptr;
-  return m.dtype == kBF16 ? row_dispatch<kBF16, GATEUP>(a, grid, lds, st)
-                          : row_dispatch<kF16, GATEUP>(a, grid, lds, st);
+  return m.dtype == kBF16 ? row_dispatch<kBF16, GATEUP>(a, S, uc, grid, lds, st)
+                          : row_dispatch<kF16, GATEUP>(a, S, uc, grid, lds, st);
 }
 
 }  // namespace
@@ -460,11 +513,12 @@ bool rowstream_enabled() {
 bool rowstream_supported(const MlpArgs& m, int stage) {
   if (m.n != 1 || (m.dtype != kBF16 && m.dtype != kF16)) return false;
   RowArgs a;
-  int grid = 0;
+  int grid = 0, S = 0, uc = 0;
   int64_t lds = 0;
-  if ((stage & kStageGateUp) && !row_plan(m.hidden, m.inter, true, m.norm_w != nullptr, m.dtype, a, grid, lds))
+  if ((stage & kStageGateUp) &&
+      !row_plan(m.hidden, m.inter, true, m.norm_w != nullptr, m.dtype, a, grid, lds, S, uc))
     return false;
-  if ((stage & kStageDown) && !row_plan(m.inter, m.hidden, false, false, m.dtype, a, grid, lds)) return false;
+  if ((stage & kStageDown) && !row_plan(m.inter, m.hidden, false, false, m.dtype, a, grid, lds, S, uc)) return false;
   // 16-byte loads of activations, weights and the norm weight; 16-byte xn stores
   const void* p16[] = {m.x, m.gate, m.up, m.down, m.tmp, m.norm_w, m.xn};
   for (const void* p : p16)
