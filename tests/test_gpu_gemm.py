@@ -48,14 +48,16 @@ def run_gemm_stages(capi, x, mats, what, cols=None):
     return out, out_ref
 
 
-@pytest.mark.parametrize("m", [96, 130, 256, 300, 513])
+@pytest.mark.parametrize("m", [16, 33, 64, 96, 130, 256, 300, 513])
 def test_gemm_partial_token_tiles(capi, m):
+    """Token counts around the tile sizes (64-token tiles up to 64 tokens,
+    then 128 and 256), with partial last tiles."""
     banner(f"gemm m={m} h=1024 i=1536")
     x, mats = make_case(m, 1024, 1536, seed=1000 + m)
     run_gemm_stages(capi, x, mats, f"m={m}")
 
 
-@pytest.mark.parametrize("h,i,m", [(1024, 3072, 128), (2048, 6144, 200), (4096, 12288, 256)])
+@pytest.mark.parametrize("h,i,m", [(1024, 3072, 128), (2048, 6144, 200), (4096, 12288, 256), (4096, 12288, 24)])
 def test_gemm_qwen3_shapes(capi, h, i, m):
     """Qwen3-0.6B, 1.7B and 8B MLP shapes."""
     banner(f"gemm qwen3 h={h} i={i} m={m}")

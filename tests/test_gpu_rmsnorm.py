@@ -76,7 +76,7 @@ def test_rmsnorm_torch_extension(capi):
     (8, 1024, 3072, SKINNY, torch.bfloat16),      # stream kernels at their token limit
     (8, 2560, 3072, SKINNY, torch.bfloat16),      # x beyond the preload registers: norm from LDS
     (2, 1024, 3072, DECODE, torch.bfloat16),      # norm kernel + fused decode kernel
-    (24, 1024, 1536, AUTO, torch.bfloat16),       # norm kernel + skinny kernels
+    (24, 1024, 1536, SKINNY, torch.bfloat16),     # norm kernel + skinny kernels
     (300, 1024, 1536, GEMM, torch.bfloat16),      # norm kernel + ring GEMM
     (130, 1024, 1536, GEMM, torch.float16),       # norm kernel + register-staged GEMM (fp16)
 ])

@@ -65,8 +65,11 @@ int validate_mlp(const MlpArgs& a, int stage) {
 }
 
 // Token count from which the tiled GEMM beats the skinny path (weights are
-// re-streamed once per 64 tokens on the skinny path).
+// re-streamed once per 64 tokens on the skinny path); for the ring GEMM's
+// shapes (bf16, K a multiple of 512) it wins from ~16 tokens (8B MLP with
+// 64-token tiles: 16 tokens 49.8 against 53.5 us, 64 tokens 56.5 against 152).
 constexpr size_t kGemmMinTokens = 96;
+constexpr size_t kRingMinTokens = 16;
 // Token count up to which the streaming decode kernels are used.
 constexpr size_t kStreamMaxTokens = 8;
 
@@ -98,7 +101,10 @@ int mlp_impl(const MlpArgs& a, int stage, int path, void* stream) {
     if (e == hipErrorNotSupported) return TI_ERR_UNSUPPORTED;
     return to_status(e);
   }
-  if (path == TI_PATH_AUTO) path = ((size_t)a.n >= kGemmMinTokens) ? TI_PATH_GEMM : TI_PATH_SKINNY;
+  if (path == TI_PATH_AUTO) {
+    const bool ring = (size_t)a.n >= kRingMinTokens && tinyinfer::gemm_ring_supported(a, stage);
+    path = ((size_t)a.n >= kGemmMinTokens || ring) ? TI_PATH_GEMM : TI_PATH_SKINNY;
+  }
   if (path == TI_PATH_GEMM) {
     if (tinyinfer::gemm_ring_supported(a, stage)) return to_status(tinyinfer::launch_gemm_ring_mlp(a, stage, s));
     return to_status(tinyinfer::launch_gemm_mlp(a, stage, s));

@@ -485,6 +485,10 @@ bool gemm_ring_supported(const MlpArgs& a, int stage) {
   return lds_cache[dev] >= RingCfg<256, 8>::kLds;
 }
 
+// Token tiles of 64 up to this many tokens (a 128-token tile would be mostly
+// padding; the tile count is the same).
+constexpr int64_t kSmallTile = 64;
+
 hipError_t launch_gemm_ring_mlp(const MlpArgs& a, int stage, hipStream_t st) {
   if (stage & kStageGateUp) {
     RingArgs r{static_cast<const uint16_t*>(a.x), {a.gate, a.up}, {a.gate_scale, a.up_scale},
@@ -496,6 +500,7 @@ hipError_t launch_gemm_ring_mlp(const MlpArgs& a, int stage, hipStream_t st) {
     hipError_t e;
     if (nw == 4) e = wr == 2 ? launch_ring<2, 128, 2, 4>(r, st) : launch_ring<2, 128, 4, 4>(r, st);
     else if (a.n > 1024) e = wr == 2 ? launch_ring<2, 256, 2>(r, st) : launch_ring<2, 256, 4>(r, st);
+    else if (a.n <= kSmallTile) e = launch_ring<2, 64, 4>(r, st);
     else e = wr == 2 ? launch_ring<2, 128, 2>(r, st) : launch_ring<2, 128, 4>(r, st);
     if (e != hipSuccess) return e;
   }
@@ -506,6 +511,7 @@ hipError_t launch_gemm_ring_mlp(const MlpArgs& a, int stage, hipStream_t st) {
     static const int wr = ring_env_wr("TINYINFER_RING_WR_DN");
     static const int nw = ring_env_nw("TINYINFER_RING_NW_DN");
     if (nw == 4) return wr == 2 ? launch_ring<1, 64, 2, 4>(r, st) : launch_ring<1, 64, 4, 4>(r, st);
+    if (a.n <= kSmallTile) return launch_ring<1, 64, 4>(r, st);
     return wr == 2 ? launch_ring<1, 128, 2>(r, st) : launch_ring<1, 128, 4>(r, st);
   }
   return hipSuccess;
