@@ -56,7 +56,8 @@ def parse():
     p.add_argument("--prefill-m", type=int, default=2048, help="prefill token count (0: skip)")
     p.add_argument("--prefill-steps", type=int, default=100)
     p.add_argument("--all", action="store_true",
-                   help="also measure every other BASELINE config (1.7B decode, 8B M=256/512, 32B 64-layer stack)")
+                   help="also measure every other BASELINE config (1.7B decode, 8B M=256/512, 32B 64-layer stack) "
+                        "and 8B small batches (M=16, 64)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline sample budget")
     p.add_argument("--copy-probe", action="store_true",
@@ -408,7 +409,7 @@ def main():
 
     points = []
     if args.all:
-        for name, ms_ in (("qwen3-1.7b", (1, 4, 8)), ("qwen3-8b", (256, 512))):
+        for name, ms_ in (("qwen3-1.7b", (1, 4, 8)), ("qwen3-8b", (16, 64, 256, 512))):
             shp = SHAPES[name]
             st = sets if name == shape.name else weight_sets(shp)
             for mm in ms_:
