@@ -55,7 +55,7 @@ def stages(capi, x, mats, what, cols=None):
     (2560, 9728),    # Qwen3-4B: last chunk 16 of 64 blocks; down 5 chunks, last 48 blocks
     (1152, 5120),    # one partial chunk of 36 blocks; down 2.5 chunks
     (8192, 1024),    # gate_up at its 4-chunk limit
-    (10240, 1024),   # gate_up beyond it: the 8-row stream kernel; down 1 chunk
+    (10240, 1024),   # gate_up beyond it: two waves per row (2 + 3 chunks); down 1 chunk
     (3072, 128),     # 16 workgroups, one row per wave; down K = 128: a 4-block chunk
     (1024, 32768),   # 16 rows per wave on a 256-CU part
     (1024, 16384),   # down K = 16384: two waves per row, 4 chunks each
@@ -191,3 +191,25 @@ def test_rowstream_down_split_override(capi, split):
         del os.environ["TINYINFER_ROW_SPLIT_DOWN"]
     assert torch.equal(out.view(torch.int16), again.view(torch.int16))
     check_close(out.cpu(), down_semantics(h.cpu(), mats[4], mats[5]), f"split {split}")
+
+
+def test_rowstream_gateup_split_with_norm(capi):
+    """gate_up split over two waves per row (TINYINFER_ROW_SPLIT_GATEUP=2) with
+    the RMSNorm prologue: each wave normalizes and writes its own chunks of
+    xn, and the output equals the unfused MLP on that xn, bit for bit."""
+    banner("rowstream gate_up split 2 + norm")
+    x, mats = make_case(1, 4096, 12288, seed=55)
+    xd, md = to_dev(x, mats)
+    w = (torch.rand(4096, generator=torch.Generator().manual_seed(4)) + 0.5).to(torch.bfloat16)
+    os.environ["TINYINFER_ROW_SPLIT_GATEUP"] = "2"
+    try:
+        out, xn = capi.mlp_forward_rmsnorm(xd, w.cuda(), 1e-6, *md, path=SKINNY)
+        plain = capi.mlp_forward(xn, *md, path=SKINNY, residual=xd)
+        torch.cuda.synchronize()
+    finally:
+        del os.environ["TINYINFER_ROW_SPLIT_GATEUP"]
+    xn_ref = om.rmsnorm_reference(x, w, 1e-6)
+    rel = ((xn.cpu().float() - xn_ref.float()).abs() / xn_ref.float().abs().clamp_min(1e-30)).max()
+    assert float(rel) <= 2 ** -7, f"xn max rel {float(rel)}"
+    assert torch.equal(out.view(torch.int16), plain.view(torch.int16))
+    assert_parity(out.cpu(), om.decoder_mlp_reference(x, w, 1e-6, *mats), "split norm + mlp")
