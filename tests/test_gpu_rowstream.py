@@ -213,3 +213,39 @@ def test_rowstream_gateup_split_with_norm(capi):
     assert float(rel) <= 2 ** -7, f"xn max rel {float(rel)}"
     assert torch.equal(out.view(torch.int16), plain.view(torch.int16))
     assert_parity(out.cpu(), om.decoder_mlp_reference(x, w, 1e-6, *mats), "split norm + mlp")
+
+
+@pytest.mark.parametrize("h,i", [
+    (4096, 12288),   # Qwen3-8B at two tokens: gate_up 2 chunks, down 3 + 3
+    (2560, 9728),    # partial chunks
+    (2048, 6144),    # Qwen3-1.7B
+    (1024, 25600),   # down over four waves (3, 3, 3, 4 chunks)
+    (1024, 4096),    # down 2 chunks, one wave per row
+])
+def test_rowstream_two_tokens(capi, h, i):
+    """Two tokens (bf16): the down stage runs on the row kernels, two MFMA
+    passes over each dequantized operand, one per token's activations (gate_up
+    on the 8-row stream kernel)."""
+    banner(f"rowstream two tokens h={h} i={i}")
+    x, mats = make_case(2, h, i, seed=5 * h + i)
+    stages(capi, x, mats, f"m=2 h={h} i={i}")
+
+
+def test_rowstream_two_tokens_norm_residual(capi):
+    """x + MLP(RMSNorm(x)) at two tokens: per-token norm sums in the prologue,
+    per-token residual in the epilogue; equal to the unfused composition."""
+    banner("rowstream two tokens norm + residual")
+    x, mats = make_case(2, 4096, 12288, seed=77)
+    xd, md = to_dev(x, mats)
+    w = (torch.rand(4096, generator=torch.Generator().manual_seed(8)) + 0.5).to(torch.bfloat16)
+    out, xn = capi.mlp_forward_rmsnorm(xd, w.cuda(), 1e-6, *md, path=SKINNY)
+    plain = capi.mlp_forward(xn, *md, path=SKINNY, residual=xd)
+    names = kernel_names(lambda: capi.mlp_forward(xn, *md, path=SKINNY, residual=xd))
+    torch.cuda.synchronize()
+    xn_ref = om.rmsnorm_reference(x, w, 1e-6)
+    rel = ((xn.cpu().float() - xn_ref.float()).abs() / xn_ref.float().abs().clamp_min(1e-30)).max()
+    assert float(rel) <= 2 ** -7, f"xn max rel {float(rel)}"
+    assert torch.equal(out.view(torch.int16), plain.view(torch.int16))
+    assert_parity(out.cpu(), om.decoder_mlp_reference(x, w, 1e-6, *mats), "m=2 norm + mlp")
+    if names:
+        assert sum("rowstream_kernel" in n for n in names) == 1, names   # down

@@ -73,13 +73,13 @@ constexpr size_t kRingMinTokens = 16;
 // Token count up to which the streaming decode kernels are used.
 constexpr size_t kStreamMaxTokens = 8;
 
-// One stage of a small batch on the best kernel that takes it: one token on
-// the row-streaming kernels, n <= 8 on the 8-row item kernels, else the
+// One stage of a small batch on the best kernel that takes it: one or two
+// tokens on the row-streaming kernels, n <= 8 on the 8-row item kernels, else the
 // 16-token-tile skinny kernels.  Chosen per stage: the two stages' K differ
 // (at 8B and n = 8 down's activations exceed the LDS the item kernel stages
 // them in, while gate_up's fit).
 hipError_t small_stage(const MlpArgs& a, int st, hipStream_t s) {
-  if (a.n == 1 && tinyinfer::rowstream_enabled() && tinyinfer::rowstream_supported(a, st))
+  if (a.n <= 2 && tinyinfer::rowstream_enabled() && tinyinfer::rowstream_supported(a, st))
     return tinyinfer::launch_rowstream_mlp(a, st, s);
   if ((size_t)a.n <= kStreamMaxTokens && tinyinfer::stream_supported(a, st))
     return tinyinfer::launch_stream_mlp(a, st, s);
@@ -198,7 +198,7 @@ int tinyinfer_mlp_forward_mxfp4_rmsnorm(const void* X, const void* norm_weight, 
     f.eps = eps;
     f.xn = xn;
     hipError_t e = hipErrorNotSupported;
-    if (f.n == 1 && tinyinfer::rowstream_enabled() && tinyinfer::rowstream_supported(f, tinyinfer::kStageGateUp))
+    if (f.n <= 2 && tinyinfer::rowstream_enabled() && tinyinfer::rowstream_supported(f, tinyinfer::kStageGateUp))
       e = tinyinfer::launch_rowstream_mlp(f, tinyinfer::kStageGateUp, s);
     else if (tinyinfer::stream_supported(f, tinyinfer::kStageGateUp))
       e = tinyinfer::launch_stream_mlp(f, tinyinfer::kStageGateUp, s);

@@ -55,12 +55,12 @@ hipError_t launch_gemm_ring_mlp(const MlpArgs& a, int stage, hipStream_t stream)
 bool stream_supported(const MlpArgs& a, int stage);
 hipError_t launch_stream_mlp(const MlpArgs& a, int stage, hipStream_t stream);
 
-// Row-streaming kernels for one token (n == 1): each load reads 1 KB of one
-// weight row, a wave owns whole rows.  rowstream_supported() says whether the
-// call fits (K % 128 == 0; K <= 8192 for gate_up, 12288 for down, fp16 6144;
-// 16-byte alignment);
-// rowstream_enabled() is false when TINYINFER_ROWSTREAM=0 (then the n <= 8
-// stream kernels serve n == 1).
+// Row-streaming kernels for one token, and for the down stage of two (bf16): each
+// load reads 1 KB of one weight row, a wave owns whole rows or a contiguous
+// share of them.  rowstream_supported() says whether the call fits (K % 128
+// == 0, activations of a wave's chunks in VGPRs, x within the LDS, 16-byte
+// alignment); rowstream_enabled() is false when TINYINFER_ROWSTREAM=0 (then
+// the n <= 8 stream kernels serve these calls).
 bool rowstream_enabled();
 bool rowstream_supported(const MlpArgs& a, int stage);
 hipError_t launch_rowstream_mlp(const MlpArgs& a, int stage, hipStream_t stream);

@@ -110,20 +110,23 @@ __device__ __forceinline__ uint32_t scale_byte(uint32_t dw) {
   return (dw >> (8 * (threadIdx.x & 3))) & 0xffu;
 }
 
-// The row's dot products (one per matrix) over chunks [cb, cb + ncs) into
-// acc, one accumulator per
-// 8-element slice t: four independent MFMA chains per matrix instead of one
+// The row's dot products (one per matrix and token: T tokens are T MFMA
+// passes over the same dequantized operand, each with that token's
+// activations) over chunks [cb, cb + ncs) into acc, one accumulator per
+// 8-element slice t (one token) or per slice pair (two tokens): independent
+// MFMA chains instead of one
 // (a chain waits out each MFMA's latency; at one token the multiply is
 // otherwise what a wave spends its time on once its rows have landed).  FULL: every lane of
 // every slot holds a real block; otherwise slots past the range (they hold a
 // repeat of its last chunk) and lanes past K multiply a zero
 // weight (scale 1.0) by the zero activation they hold.  FAST: every scale
 // byte in the hardware conversion's exact range.
-template <int DT, int UC, bool GATEUP, bool FAST, bool FULL>
+template <int DT, int UC, bool GATEUP, bool FAST, bool FULL, int T>
 __device__ __forceinline__ void mma_row(const RowArgs& a, int cb, int ncs, const RowBuf<UC, GATEUP>& b,
-                                        const u32x4_t (&xr)[UC][4], const u32x4_t (&xl)[UC][4],
-                                        f32x4_t (&acc)[2][4]) {
+                                        const u32x4_t (&xr)[T][UC][4], const u32x4_t (&xl)[T][UC][4],
+                                        f32x4_t (&acc)[2][T][4 / T]) {
   constexpr int kMats = GATEUP ? 2 : 1;
+  constexpr int kCh = 4 / T;                  // accumulator chains per (matrix, token)
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int m = 0; m < kMats; ++m) {
@@ -135,10 +138,14 @@ __device__ __forceinline__ void mma_row(const RowArgs& a, int cb, int ncs, const
       for (int t = 0; t < 4; ++t) {
         const uint32_t wq = valid ? b.w[m * UC + q][t] : 0u;
         const u32x4_t wa = FAST ? dq8_bf16_fast(wq, sb) : dq8_bf16_exact(wq, sb);
-        if constexpr (DT == kBF16) {
-          acc[m][t] = mfma16x16x32(wa, xr[q][t], acc[m][t]);
-        } else {
-          acc[m][t] = mfma16x16x32(wa, xl[q][t], mfma16x16x32(wa, xr[q][t], acc[m][t]));
+#pragma unroll
+        for (int tk = 0; tk < T; ++tk) {
+          f32x4_t& c = acc[m][tk][t % kCh];
+          if constexpr (DT == kBF16) {
+            c = mfma16x16x32(wa, xr[tk][q][t], c);
+          } else {
+            c = mfma16x16x32(wa, xl[tk][q][t], mfma16x16x32(wa, xr[tk][q][t], c));
+          }
         }
       }
     }
@@ -169,11 +176,13 @@ __device__ __forceinline__ float diag_sum(const f32x4_t& c) {
 // S waves share each row (S divides the workgroup's 8 waves): wave s of the
 // group multiplies chunks [s nc / S, (s + 1) nc / S) and the S partial sums
 // are added in order at the end.  UC is the largest share.
-template <int DT, int UC, bool GATEUP, int S>
+template <int DT, int UC, bool GATEUP, int S, int T>
 __global__ __launch_bounds__(kRThreads, 1) void rowstream_kernel(RowArgs a) {
   static_assert(kRW % S == 0, "the waves sharing a row are in one workgroup");
-  // 16-byte x chunks per thread: K / 8 <= 256 UC S (x is staged whole)
-  constexpr int kXPre = (256 * UC * S + kRThreads - 1) / kRThreads;
+  static_assert(T == 1 || (T == 2 && DT == kBF16), "one token, or two in bf16");
+  // 16-byte x chunks per thread: T K / 8 <= 256 UC S T (x is staged whole)
+  constexpr int kXPre = (256 * UC * S * T + kRThreads - 1) / kRThreads;
+  constexpr int kCh = 4 / T;
   extern __shared__ __align__(16) uint8_t lds[];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -185,8 +194,10 @@ __global__ __launch_bounds__(kRThreads, 1) void rowstream_kernel(RowArgs a) {
   const int rows = slot < a.R ? (a.R - slot + nslots - 1) / nslots : 0;
 
   // Prologue loads, issued before the first weights (loads complete in
-  // issue order): x, and the norm weight when there is one.
-  const int nxc = a.K / 8;
+  // issue order): x ([T, K], rows contiguous), and the norm weight when there
+  // is one.
+  const int nxr = a.K / 8;                   // 16-byte chunks per token row
+  const int nxc = T * nxr;
   const bool norm = GATEUP && a.norm_w != nullptr;
   u32x4_t xv[kXPre], nv[kXPre];
 #pragma unroll
@@ -198,7 +209,7 @@ __global__ __launch_bounds__(kRThreads, 1) void rowstream_kernel(RowArgs a) {
 #pragma unroll
     for (int p = 0; p < kXPre; ++p) {
       const int c = threadIdx.x + p * kRThreads;
-      nv[p] = *reinterpret_cast<const u32x4_t*>(a.norm_w + 8 * (c < nxc ? c : nxc - 1));
+      nv[p] = *reinterpret_cast<const u32x4_t*>(a.norm_w + 8 * (c < nxr ? c : nxr - 1));
     }
   }
 
@@ -213,35 +224,46 @@ __global__ __launch_bounds__(kRThreads, 1) void rowstream_kernel(RowArgs a) {
   issue_row<UC, GATEUP>(a, row_of(0), cb, ncs, b0);
   issue_row<UC, GATEUP>(a, row_of(1), cb, ncs, b1);
 
-  // LDS position of 16-byte x chunk c (elements 8c .. 8c+7 = slice c % 4 of
-  // block c / 4): slice-major, so the copy into registers below, where lane l
-  // reads slice t of its block, touches consecutive 16-byte words
+  // LDS position of 16-byte x chunk c of a token row (elements 8c .. 8c+7 =
+  // slice c % 4 of block c / 4): slice-major, so the copy into registers
+  // below, where lane l reads slice t of its block, touches consecutive
+  // 16-byte words; token rows 2K bytes apart
   const int plane = a.K / 2;                 // bytes per slice plane
   auto xpos = [&](int c) { return (c & 3) * plane + 16 * (c >> 2); };
   // x (and the norm weight) into LDS; with a norm, each wave's sum of the
-  // squares of the chunks it loaded (fixed order: per thread, then the wave)
-  float* nsum = reinterpret_cast<float*>(lds + a.lds_sum);
-  float sq = 0.f;
+  // squares of the chunks it loaded, per token (fixed order: per thread,
+  // then the wave)
+  float* nsum = reinterpret_cast<float*>(lds + a.lds_sum);   // [kRW][T]
+  float sq[T];
+#pragma unroll
+  for (int tk = 0; tk < T; ++tk) sq[tk] = 0.f;
 #pragma unroll
   for (int p = 0; p < kXPre; ++p) {
     const int c = threadIdx.x + p * kRThreads;
     if (c < nxc) {
-      *reinterpret_cast<u32x4_t*>(lds + xpos(c)) = xv[p];
+      const int tk = c / nxr, cc = c - tk * nxr;
+      *reinterpret_cast<u32x4_t*>(lds + tk * 2 * a.K + xpos(cc)) = xv[p];
       if (norm) {
-        *reinterpret_cast<u32x4_t*>(lds + a.lds_nw + xpos(c)) = nv[p];
+        if (c < nxr) *reinterpret_cast<u32x4_t*>(lds + a.lds_nw + xpos(c)) = nv[p];
+        float s2 = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const float lo = act_to_f32<DT>((uint16_t)(xv[p][j] & 0xffffu));
           const float hi = act_to_f32<DT>((uint16_t)(xv[p][j] >> 16));
-          sq += lo * lo;
-          sq += hi * hi;
+          s2 += lo * lo;
+          s2 += hi * hi;
         }
+#pragma unroll
+        for (int t2 = 0; t2 < T; ++t2) sq[t2] += t2 == tk ? s2 : 0.f;
       }
     }
   }
   if (norm) {
-    sq = wave_sum64(sq);
-    if (lane == 0) nsum[wave] = sq;
+#pragma unroll
+    for (int tk = 0; tk < T; ++tk) {
+      const float w = wave_sum64(sq[tk]);
+      if (lane == 0) nsum[wave * T + tk] = w;
+    }
   }
   // every wave's LDS stores are done before any wave reads them: wait for
   // LDS only (a full __syncthreads would also wait for the weights in flight)
@@ -252,67 +274,86 @@ __global__ __launch_bounds__(kRThreads, 1) void rowstream_kernel(RowArgs a) {
 
   // the reference's post_attention_layernorm (tinyinfer/csrc/rmsnorm.cu:10-54):
   // inv = rsqrt(sum / K + eps), the same in every wave and workgroup
-  float inv = 1.f;
-  if (norm) {
-    float tot = 0.f;
+  float inv[T];
 #pragma unroll
-    for (int w = 0; w < kRW; ++w) tot += nsum[w];
-    inv = rsqrtf(tot / (float)a.K + a.eps);
+  for (int tk = 0; tk < T; ++tk) {
+    inv[tk] = 1.f;
+    if (norm) {
+      float tot = 0.f;
+#pragma unroll
+      for (int w = 0; w < kRW; ++w) tot += nsum[w * T + tk];
+      inv[tk] = rsqrtf(tot / (float)a.K + a.eps);
+    }
   }
 
   // lane l's activations: block 64c + l of each of its chunks c = cb + q,
   // zero past K; with a norm, x <- round(w * x * inv).  fp16 is split into
   // exact bf16 hi + lo.
-  u32x4_t xr[UC][4], xl[UC][4];
+  u32x4_t xr[T][UC][4], xl[T][UC][4];
 #pragma unroll
-  for (int q = 0; q < UC; ++q) {
-    const int blk = (cb + q) * kChunkBlocks + lane;
-    const bool valid = q < ncs && blk < a.nblk;
-    const int bc = valid ? blk : 0;
+  for (int tk = 0; tk < T; ++tk) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      u32x4_t v = *reinterpret_cast<const u32x4_t*>(lds + xpos(4 * bc + t));
-      if (norm) {
-        const u32x4_t g = *reinterpret_cast<const u32x4_t*>(lds + a.lds_nw + xpos(4 * bc + t));
+    for (int q = 0; q < UC; ++q) {
+      const int blk = (cb + q) * kChunkBlocks + lane;
+      const bool valid = q < ncs && blk < a.nblk;
+      const int bc = valid ? blk : 0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float lo = act_to_f32<DT>((uint16_t)(g[j] & 0xffffu)) * act_to_f32<DT>((uint16_t)(v[j] & 0xffffu)) * inv;
-          const float hi = act_to_f32<DT>((uint16_t)(g[j] >> 16)) * act_to_f32<DT>((uint16_t)(v[j] >> 16)) * inv;
-          v[j] = (uint32_t)f32_to_act<DT>(lo) | ((uint32_t)f32_to_act<DT>(hi) << 16);
+      for (int t = 0; t < 4; ++t) {
+        u32x4_t v = *reinterpret_cast<const u32x4_t*>(lds + tk * 2 * a.K + xpos(4 * bc + t));
+        if (norm) {
+          const u32x4_t g = *reinterpret_cast<const u32x4_t*>(lds + a.lds_nw + xpos(4 * bc + t));
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float lo =
+                act_to_f32<DT>((uint16_t)(g[j] & 0xffffu)) * act_to_f32<DT>((uint16_t)(v[j] & 0xffffu)) * inv[tk];
+            const float hi = act_to_f32<DT>((uint16_t)(g[j] >> 16)) * act_to_f32<DT>((uint16_t)(v[j] >> 16)) * inv[tk];
+            v[j] = (uint32_t)f32_to_act<DT>(lo) | ((uint32_t)f32_to_act<DT>(hi) << 16);
+          }
         }
-      }
-      if (!valid) v = u32x4_t{0u, 0u, 0u, 0u};
-      if constexpr (DT == kBF16) {
-        xr[q][t] = v;
-        xl[q][t] = v;
-      } else {
-        f16x8_split_bf16(v, xr[q][t], xl[q][t]);
+        if (!valid) v = u32x4_t{0u, 0u, 0u, 0u};
+        if constexpr (DT == kBF16) {
+          xr[tk][q][t] = v;
+          xl[tk][q][t] = v;
+        } else {
+          f16x8_split_bf16(v, xr[tk][q][t], xl[tk][q][t]);
+        }
       }
     }
   }
 
-  float* outs = reinterpret_cast<float*>(lds + a.lds_out);   // [rows_max][kRW][2] partial sums
+  float* outs = reinterpret_cast<float*>(lds + a.lds_out);   // [rows_max][kRW][T][2] partial sums
   // multiply row j from buffer b; with ISSUE, then load row j + 2 into b
   auto step = [&](RowBuf<UC, GATEUP>& b, int j, auto issue_tag) {
-    f32x4_t acc[2][4];
+    f32x4_t acc[2][T][kCh];
 #pragma unroll
     for (int m = 0; m < 2; ++m)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) acc[m][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int tk = 0; tk < T; ++tk)
+#pragma unroll
+        for (int c = 0; c < kCh; ++c) acc[m][tk][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     bool ok = true;
 #pragma unroll
     for (int k = 0; k < RowBuf<UC, GATEUP>::kMats * UC; ++k) ok = ok && e8m0_fast_ok(scale_byte(b.s[k]));
     if (wave_all(ok)) {
-      if (a.full && ncs == UC) mma_row<DT, UC, GATEUP, true, true>(a, cb, ncs, b, xr, xl, acc);
-      else mma_row<DT, UC, GATEUP, true, false>(a, cb, ncs, b, xr, xl, acc);
+      if (a.full && ncs == UC) mma_row<DT, UC, GATEUP, true, true, T>(a, cb, ncs, b, xr, xl, acc);
+      else mma_row<DT, UC, GATEUP, true, false, T>(a, cb, ncs, b, xr, xl, acc);
     } else {
-      mma_row<DT, UC, GATEUP, false, false>(a, cb, ncs, b, xr, xl, acc);
+      mma_row<DT, UC, GATEUP, false, false, T>(a, cb, ncs, b, xr, xl, acc);
     }
     if constexpr (decltype(issue_tag)::value) issue_row<UC, GATEUP>(a, row_of(j + 2), cb, ncs, b);
-    const float y0 = diag_sum((acc[0][0] + acc[0][1]) + (acc[0][2] + acc[0][3]));
-    float y1 = 0.f;
-    if constexpr (GATEUP) y1 = diag_sum((acc[1][0] + acc[1][1]) + (acc[1][2] + acc[1][3]));
-    if (lane == 0) *reinterpret_cast<f32x2_t*>(outs + 2 * (j * kRW + wave)) = f32x2_t{y0, y1};
+    auto chains = [&](int m, int tk) {
+      f32x4_t c = acc[m][tk][0];
+#pragma unroll
+      for (int i = 1; i < kCh; ++i) c += acc[m][tk][i];
+      return c;
+    };
+#pragma unroll
+    for (int tk = 0; tk < T; ++tk) {
+      const float y0 = diag_sum(chains(0, tk));
+      float y1 = 0.f;
+      if constexpr (GATEUP) y1 = diag_sum(chains(1, tk));
+      if (lane == 0) *reinterpret_cast<f32x2_t*>(outs + 2 * ((j * kRW + wave) * T + tk)) = f32x2_t{y0, y1};
+    }
   };
   constexpr std::true_type kIssue{};
   constexpr std::false_type kLast{};
@@ -343,31 +384,36 @@ __global__ __launch_bounds__(kRThreads, 1) void rowstream_kernel(RowArgs a) {
   // would make the load-queue accounting path-dependent): the S parts of a
   // row added in order, then the epilogue; 8 / S consecutive rows per j
   __syncthreads();
-  for (int i = threadIdx.x; i < a.rows_max * (kRW / S); i += kRThreads) {
-    const int jj = i / (kRW / S), sl = i - jj * (kRW / S);
+  for (int i = threadIdx.x; i < a.rows_max * (kRW / S) * T; i += kRThreads) {
+    const int tk = i % T, i2 = i / T;
+    const int jj = i2 / (kRW / S), sl = i2 - jj * (kRW / S);
     const int64_t row = (int64_t)blockIdx.x * (kRW / S) + sl + (int64_t)jj * nslots;
     if (row < a.R) {
       float y0 = 0.f, y1 = 0.f;
 #pragma unroll
       for (int p = 0; p < S; ++p) {
-        const f32x2_t v = *reinterpret_cast<const f32x2_t*>(outs + 2 * (jj * kRW + sl * S + p));
+        const f32x2_t v = *reinterpret_cast<const f32x2_t*>(outs + 2 * ((jj * kRW + sl * S + p) * T + tk));
         y0 += v[0];
         y1 += v[1];
       }
       const float v = GATEUP ? silu_f32(y0) * y1 : y0;
-      a.out[row] = with_residual<DT>(f32_to_act<DT>(v), a.res, row);
+      const int64_t o = (int64_t)tk * a.R + row;
+      a.out[o] = with_residual<DT>(f32_to_act<DT>(v), a.res, o);
     }
   }
   if (norm && blockIdx.x == 0 && wave < S && a.xn) {
 #pragma unroll
-    for (int q = 0; q < UC; ++q) {
-      const int blk = (cb + q) * kChunkBlocks + lane;
-      if (q < ncs && blk < a.nblk) {
+    for (int tk = 0; tk < T; ++tk) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          u32x4_t v = xr[q][t];
-          if constexpr (DT != kBF16) v = join_f16x8(xr[q][t], xl[q][t]);
-          *reinterpret_cast<u32x4_t*>(a.xn + 32 * blk + 8 * t) = v;
+      for (int q = 0; q < UC; ++q) {
+        const int blk = (cb + q) * kChunkBlocks + lane;
+        if (q < ncs && blk < a.nblk) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            u32x4_t v = xr[tk][q][t];
+            if constexpr (DT != kBF16) v = join_f16x8(xr[tk][q][t], xl[tk][q][t]);
+            *reinterpret_cast<u32x4_t*>(a.xn + (int64_t)tk * a.K + 32 * blk + 8 * t) = v;
+          }
         }
       }
     }
@@ -400,13 +446,19 @@ int split_env(const char* name) {
 // matrices in flight; down 6; fp16 3, its activations are held as hi + lo)
 // and, for down, holds at most 3 chunks where possible; or the S that
 // TINYINFER_ROW_SPLIT_GATEUP / _DOWN names, if that fits.
-bool row_plan(int64_t K, int64_t R, bool gateup, bool norm, int dtype, RowArgs& a, int& grid, int64_t& lds,
-              int& S, int& uc) {
+bool row_plan(int64_t M, int64_t K, int64_t R, bool gateup, bool norm, int dtype, RowArgs& a, int& grid,
+              int64_t& lds, int& S, int& uc) {
   const int cus = row_cus();
   // K % 128: scale rows start dword-aligned
   if (cus < 1 || K < 128 || K % 128 != 0 || K > (1 << 20) || R < 1 || R > (1 << 24)) return false;
+  if (M < 1 || M > 2 || (M == 2 && dtype != kBF16)) return false;
+  // two tokens double the multiply per row: gate_up (two matrices) measured
+  // 13.06 us on these kernels against 12.82 on the 8-row stream kernel at 8B;
+  // down 7.76 against 9.13
+  if (M == 2 && gateup) return false;
   const int nc = (int)((K + kChunkK - 1) / kChunkK);
-  const int ucmax = dtype != kBF16 ? 3 : gateup ? 4 : kMaxUC;
+  // chunks per wave: activations of every chunk and token stay in VGPRs
+  const int ucmax = dtype != kBF16 ? 3 : M == 2 ? (gateup ? 2 : 3) : gateup ? 4 : kMaxUC;
   const int smax = gateup ? 2 : 4;
   S = 0;
   const int want = split_env(gateup ? "TINYINFER_ROW_SPLIT_GATEUP" : "TINYINFER_ROW_SPLIT_DOWN");
@@ -429,21 +481,21 @@ bool row_plan(int64_t K, int64_t R, bool gateup, bool norm, int dtype, RowArgs& 
   a.nblk = (int)(K / kBlock);
   a.full = K % kChunkK == 0;
   a.rows_max = (int)((R + nslots - 1) / nslots);
-  int64_t off = K * 2;                       // x
+  int64_t off = M * K * 2;                   // x
   a.lds_nw = (int)off;
   if (gateup && norm) off += K * 2;          // norm weight
   off = (off + 15) & ~int64_t(15);
   a.lds_sum = (int)off;
-  off += 4 * kRW;
+  off += 4 * kRW * M;
   a.lds_out = (int)off;
-  off += 8 * (int64_t)a.rows_max * kRW;      // two fp32 partial sums per (row, wave)
+  off += 8 * (int64_t)a.rows_max * kRW * M;  // two fp32 partial sums per (row, wave, token)
   lds = (off + 15) & ~int64_t(15);
   return lds <= 160 * 1024;
 }
 
-template <int DT, int UC, bool GATEUP, int S>
+template <int DT, int UC, bool GATEUP, int S, int T>
 hipError_t row_launch(const RowArgs& a, int grid, int64_t lds, hipStream_t st) {
-  auto k = rowstream_kernel<DT, UC, GATEUP, S>;
+  auto k = rowstream_kernel<DT, UC, GATEUP, S, T>;
   if (lds > 64 * 1024 &&
       hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
           hipSuccess)
@@ -452,29 +504,29 @@ hipError_t row_launch(const RowArgs& a, int grid, int64_t lds, hipStream_t st) {
   return hipGetLastError();
 }
 
-// The instantiated (UC, S) pairs: gate_up S = 1, UC <= 4; down S = 1, 2, 4
-// with UC <= 6 (fp16: UC <= 3).
-template <int DT, bool GATEUP, int S>
+// The instantiated (UC, S, T): one token: gate_up S = 1, 2 with UC <= 4, down
+// S = 1, 2, 4 with UC <= 6 (fp16 UC <= 3); two tokens (bf16): down UC <= 3.
+template <int DT, bool GATEUP, int S, int T>
 hipError_t row_dispatch_s(const RowArgs& a, int uc, int grid, int64_t lds, hipStream_t st) {
-  constexpr int kMax = DT != kBF16 ? 3 : GATEUP ? 4 : kMaxUC;
+  constexpr int kMax = DT != kBF16 ? 3 : T == 2 ? (GATEUP ? 2 : 3) : GATEUP ? 4 : kMaxUC;
   switch (uc) {
-    case 1: if constexpr (S == 1 || GATEUP) return row_launch<DT, 1, GATEUP, S>(a, grid, lds, st); break;
-    case 2: return row_launch<DT, 2, GATEUP, S>(a, grid, lds, st);
-    case 3: return row_launch<DT, 3, GATEUP, S>(a, grid, lds, st);
-    case 4: if constexpr (kMax >= 4) return row_launch<DT, 4, GATEUP, S>(a, grid, lds, st); break;
-    case 5: if constexpr (kMax >= 5) return row_launch<DT, 5, GATEUP, S>(a, grid, lds, st); break;
-    case 6: if constexpr (kMax >= 6) return row_launch<DT, 6, GATEUP, S>(a, grid, lds, st); break;
+    case 1: if constexpr (S == 1 || GATEUP) return row_launch<DT, 1, GATEUP, S, T>(a, grid, lds, st); break;
+    case 2: return row_launch<DT, 2, GATEUP, S, T>(a, grid, lds, st);
+    case 3: if constexpr (kMax >= 3) return row_launch<DT, 3, GATEUP, S, T>(a, grid, lds, st); break;
+    case 4: if constexpr (kMax >= 4) return row_launch<DT, 4, GATEUP, S, T>(a, grid, lds, st); break;
+    case 5: if constexpr (kMax >= 5) return row_launch<DT, 5, GATEUP, S, T>(a, grid, lds, st); break;
+    case 6: if constexpr (kMax >= 6) return row_launch<DT, 6, GATEUP, S, T>(a, grid, lds, st); break;
     default: break;
   }
   return hipErrorNotSupported;
 }
 
-template <int DT, bool GATEUP>
+template <int DT, bool GATEUP, int T>
 hipError_t row_dispatch(const RowArgs& a, int S, int uc, int grid, int64_t lds, hipStream_t st) {
-  if (S == 1) return row_dispatch_s<DT, GATEUP, 1>(a, uc, grid, lds, st);
-  if (S == 2) return row_dispatch_s<DT, GATEUP, 2>(a, uc, grid, lds, st);
+  if (S == 1) return row_dispatch_s<DT, GATEUP, 1, T>(a, uc, grid, lds, st);
+  if (S == 2) return row_dispatch_s<DT, GATEUP, 2, T>(a, uc, grid, lds, st);
   if constexpr (!GATEUP) {
-    if (S == 4) return row_dispatch_s<DT, GATEUP, 4>(a, uc, grid, lds, st);
+    if (S == 4) return row_dispatch_s<DT, GATEUP, 4, T>(a, uc, grid, lds, st);
   }
   return hipErrorNotSupported;
 }
@@ -488,7 +540,7 @@ hipError_t row_stage(const MlpArgs& m, hipStream_t st) {
   const int64_t R = GATEUP ? m.inter : m.hidden;
   const bool norm = GATEUP && m.norm_w != nullptr;
   int S = 0, uc = 0;
-  if (!row_plan(K, R, GATEUP, norm, m.dtype, a, grid, lds, S, uc)) return hipErrorNotSupported;
+  if (!row_plan(m.n, K, R, GATEUP, norm, m.dtype, a, grid, lds, S, uc)) return hipErrorNotSupported;
   a.x = static_cast<const uint16_t*>(GATEUP ? m.x : m.tmp);
   a.w0 = GATEUP ? m.gate : m.down;
   a.s0 = GATEUP ? m.gate_scale : m.down_scale;
@@ -499,8 +551,11 @@ hipError_t row_stage(const MlpArgs& m, hipStream_t st) {
   a.norm_w = norm ? static_cast<const uint16_t*>(m.norm_w) : nullptr;
   a.eps = m.eps;
   a.xn = norm ? static_cast<uint16_t*>(m.xn) : nullptr;
-  return m.dtype == kBF16 ? row_dispatch<kBF16, GATEUP>(a, S, uc, grid, lds, st)
-                          : row_dispatch<kF16, GATEUP>(a, S, uc, grid, lds, st);
+  if (m.dtype != kBF16) return row_dispatch<kF16, GATEUP, 1>(a, S, uc, grid, lds, st);
+  if constexpr (!GATEUP) {
+    if (m.n == 2) return row_dispatch<kBF16, GATEUP, 2>(a, S, uc, grid, lds, st);
+  }
+  return row_dispatch<kBF16, GATEUP, 1>(a, S, uc, grid, lds, st);
 }
 
 }  // namespace
@@ -511,14 +566,15 @@ bool rowstream_enabled() {
 }
 
 bool rowstream_supported(const MlpArgs& m, int stage) {
-  if (m.n != 1 || (m.dtype != kBF16 && m.dtype != kF16)) return false;
+  if (m.n < 1 || m.n > 2 || (m.dtype != kBF16 && m.dtype != kF16)) return false;
   RowArgs a;
   int grid = 0, S = 0, uc = 0;
   int64_t lds = 0;
   if ((stage & kStageGateUp) &&
-      !row_plan(m.hidden, m.inter, true, m.norm_w != nullptr, m.dtype, a, grid, lds, S, uc))
+      !row_plan(m.n, m.hidden, m.inter, true, m.norm_w != nullptr, m.dtype, a, grid, lds, S, uc))
     return false;
-  if ((stage & kStageDown) && !row_plan(m.inter, m.hidden, false, false, m.dtype, a, grid, lds, S, uc)) return false;
+  if ((stage & kStageDown) && !row_plan(m.n, m.inter, m.hidden, false, false, m.dtype, a, grid, lds, S, uc))
+    return false;
   // 16-byte loads of activations, weights and the norm weight; 16-byte xn stores
   const void* p16[] = {m.x, m.gate, m.up, m.down, m.tmp, m.norm_w, m.xn};
   for (const void* p : p16)
