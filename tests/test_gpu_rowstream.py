@@ -222,18 +222,21 @@ def test_rowstream_gateup_split_with_norm(capi):
     (1024, 25600),   # down over four waves (3, 3, 3, 4 chunks)
     (1024, 4096),    # down 2 chunks, one wave per row
 ])
-def test_rowstream_two_tokens(capi, h, i):
-    """Two tokens (bf16): the down stage runs on the row kernels, two MFMA
-    passes over each dequantized operand, one per token's activations (gate_up
-    on the 8-row stream kernel)."""
+def test_rowstream_two_tokens(capi, h, i, monkeypatch):
+    """Two tokens (bf16) with the row-pair kernels off: the down stage runs on
+    the row kernels, two MFMA passes over each dequantized operand, one per
+    token's activations (gate_up on the 8-row stream kernel)."""
+    monkeypatch.setenv("TINYINFER_ROWPAIR", "0")
     banner(f"rowstream two tokens h={h} i={i}")
     x, mats = make_case(2, h, i, seed=5 * h + i)
     stages(capi, x, mats, f"m=2 h={h} i={i}")
 
 
-def test_rowstream_two_tokens_norm_residual(capi):
-    """x + MLP(RMSNorm(x)) at two tokens: per-token norm sums in the prologue,
-    per-token residual in the epilogue; equal to the unfused composition."""
+def test_rowstream_two_tokens_norm_residual(capi, monkeypatch):
+    """x + MLP(RMSNorm(x)) at two tokens (row-pair kernels off): per-token
+    norm sums in the prologue, per-token residual in the epilogue; equal to
+    the unfused composition."""
+    monkeypatch.setenv("TINYINFER_ROWPAIR", "0")
     banner("rowstream two tokens norm + residual")
     x, mats = make_case(2, 4096, 12288, seed=77)
     xd, md = to_dev(x, mats)

@@ -30,6 +30,14 @@ def capi():
     return c
 
 
+@pytest.fixture(autouse=True)
+def stream_kernels_only(monkeypatch):
+    """The row and row-pair kernels take 1..4 tokens when they are on; these
+    tests keep them off so that every case runs on the 8-row stream kernels."""
+    monkeypatch.setenv("TINYINFER_ROWSTREAM", "0")
+    monkeypatch.setenv("TINYINFER_ROWPAIR", "0")
+
+
 def h_semantics(x, gp, gs, up, us):
     """Exact gate/up sums, SiLU(g)*u rounded once to the activation dtype."""
     x64 = x.to(torch.float64).numpy()

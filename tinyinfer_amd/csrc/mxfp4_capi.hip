@@ -79,6 +79,8 @@ constexpr size_t kStreamMaxTokens = 8;
 // (at 8B and n = 8 down's activations exceed the LDS the item kernel stages
 // them in, while gate_up's fit).
 hipError_t small_stage(const MlpArgs& a, int st, hipStream_t s) {
+  if (a.n >= 2 && a.n <= 4 && tinyinfer::rowpair_enabled() && tinyinfer::rowpair_supported(a, st))
+    return tinyinfer::launch_rowpair_mlp(a, st, s);
   if (a.n <= 2 && tinyinfer::rowstream_enabled() && tinyinfer::rowstream_supported(a, st))
     return tinyinfer::launch_rowstream_mlp(a, st, s);
   if ((size_t)a.n <= kStreamMaxTokens && tinyinfer::stream_supported(a, st))
@@ -198,7 +200,10 @@ int tinyinfer_mlp_forward_mxfp4_rmsnorm(const void* X, const void* norm_weight, 
     f.eps = eps;
     f.xn = xn;
     hipError_t e = hipErrorNotSupported;
-    if (f.n <= 2 && tinyinfer::rowstream_enabled() && tinyinfer::rowstream_supported(f, tinyinfer::kStageGateUp))
+    // the same kernel order as small_stage (the skinny kernels have no norm prologue)
+    if (f.n >= 2 && f.n <= 4 && tinyinfer::rowpair_enabled() && tinyinfer::rowpair_supported(f, tinyinfer::kStageGateUp))
+      e = tinyinfer::launch_rowpair_mlp(f, tinyinfer::kStageGateUp, s);
+    else if (f.n <= 2 && tinyinfer::rowstream_enabled() && tinyinfer::rowstream_supported(f, tinyinfer::kStageGateUp))
       e = tinyinfer::launch_rowstream_mlp(f, tinyinfer::kStageGateUp, s);
     else if (tinyinfer::stream_supported(f, tinyinfer::kStageGateUp))
       e = tinyinfer::launch_stream_mlp(f, tinyinfer::kStageGateUp, s);

@@ -65,6 +65,13 @@ bool rowstream_enabled();
 bool rowstream_supported(const MlpArgs& a, int stage);
 hipError_t launch_rowstream_mlp(const MlpArgs& a, int stage, hipStream_t stream);
 
+// Row-pair kernels for 2..4 tokens (bf16): each load reads 512 B of each of
+// two weight rows, one MFMA serves two tokens.  rowpair_supported() says
+// whether the call fits; rowpair_enabled() is false when TINYINFER_ROWPAIR=0.
+bool rowpair_enabled();
+bool rowpair_supported(const MlpArgs& a, int stage);
+hipError_t launch_rowpair_mlp(const MlpArgs& a, int stage, hipStream_t stream);
+
 // Fused decode kernel (gate_up, cross-workgroup flags, down in one launch)
 // for n <= 4 tokens; hipErrorNotSupported when the shape, alignment or the
 // device's LDS/occupancy do not allow it.
