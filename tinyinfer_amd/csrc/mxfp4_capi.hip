@@ -72,9 +72,12 @@ constexpr size_t kGemmMinTokens = 96;
 constexpr size_t kRingMinTokens = 16;
 // Token count up to which the streaming decode kernels are used.
 constexpr size_t kStreamMaxTokens = 8;
+// split-K tile kernels: up to 64 tokens (four 16-token MFMA column tiles)
+constexpr size_t kTileMaxTokens = 64;
 
-// One stage of a small batch on the best kernel that takes it: one or two
-// tokens on the row-streaming kernels, n <= 8 on the 8-row item kernels, else the
+// One stage of a small batch on the best kernel that takes it: 2..4 tokens on
+// the row-pair kernels, one or two on the row-streaming kernels, n <= 8 on the
+// 8-row item kernels, n <= 64 on the split-K tile kernels, else the
 // 16-token-tile skinny kernels.  Chosen per stage: the two stages' K differ
 // (at 8B and n = 8 down's activations exceed the LDS the item kernel stages
 // them in, while gate_up's fit).
@@ -85,6 +88,8 @@ hipError_t small_stage(const MlpArgs& a, int st, hipStream_t s) {
     return tinyinfer::launch_rowstream_mlp(a, st, s);
   if ((size_t)a.n <= kStreamMaxTokens && tinyinfer::stream_supported(a, st))
     return tinyinfer::launch_stream_mlp(a, st, s);
+  if ((size_t)a.n <= kTileMaxTokens && tinyinfer::tile_enabled() && tinyinfer::tile_supported(a, st, s))
+    return tinyinfer::launch_tile_mlp(a, st, s);
   return tinyinfer::launch_skinny_mlp(a, st, s);
 }
 
@@ -104,8 +109,10 @@ int mlp_impl(const MlpArgs& a, int stage, int path, void* stream) {
     return to_status(e);
   }
   if (path == TI_PATH_AUTO) {
+    const bool tile = (size_t)a.n <= kTileMaxTokens && tinyinfer::tile_enabled() &&
+                      tinyinfer::tile_supported(a, stage, s);
     const bool ring = (size_t)a.n >= kRingMinTokens && tinyinfer::gemm_ring_supported(a, stage);
-    path = ((size_t)a.n >= kGemmMinTokens || ring) ? TI_PATH_GEMM : TI_PATH_SKINNY;
+    path = ((size_t)a.n >= kGemmMinTokens || (ring && !tile)) ? TI_PATH_GEMM : TI_PATH_SKINNY;
   }
   if (path == TI_PATH_GEMM) {
     if (tinyinfer::gemm_ring_supported(a, stage)) return to_status(tinyinfer::launch_gemm_ring_mlp(a, stage, s));

@@ -517,4 +517,6 @@ hipError_t launch_gemm_ring_mlp(const MlpArgs& a, int stage, hipStream_t st) {
   return hipSuccess;
 }
 
+float* gemm_split_workspace(size_t bytes, hipStream_t st) { return split_workspace(bytes, st); }
+
 }  // namespace tinyinfer

@@ -72,6 +72,22 @@ bool rowpair_enabled();
 bool rowpair_supported(const MlpArgs& a, int stage);
 hipError_t launch_rowpair_mlp(const MlpArgs& a, int stage, hipStream_t stream);
 
+// Split-K tile kernels for 5..64 tokens (bf16, K % 1024 == 0): a workgroup
+// owns one 1024-element K range (its activations staged once in LDS) and
+// streams 16-row weight groups through MFMA; a reduce launch adds the K
+// ranges in order and applies the epilogue.  tile_supported() says whether
+// the call fits and its fp32 workspace can be had (not during graph capture
+// unless the stream's workspace is already large enough); tile_enabled() is
+// false when TINYINFER_TILE=0.
+bool tile_enabled();
+bool tile_supported(const MlpArgs& a, int stage, hipStream_t stream);
+hipError_t launch_tile_mlp(const MlpArgs& a, int stage, hipStream_t stream);
+
+// The split-K workspace of the prefill GEMM: one fp32 buffer per (device,
+// stream), grown on demand, never freed; null when it cannot grow (graph
+// capture, allocation failure).
+float* gemm_split_workspace(size_t bytes, hipStream_t stream);
+
 // Fused decode kernel (gate_up, cross-workgroup flags, down in one launch)
 // for n <= 4 tokens; hipErrorNotSupported when the shape, alignment or the
 // device's LDS/occupancy do not allow it.

@@ -1,0 +1,344 @@
+// Split-K tile kernels for small batches (5..64 bf16 tokens): the reference's
+// per-token GEMV stages mlp_stage1_mxfp4 / mlp_stage2_mxfp4
+// (tinyinfer/csrc/mlp_fp4.cu:79-142, 365-426) for a batch whose activations
+// are too many for the decode kernels' registers and too few for the
+// prefill GEMM's 64-token tiles to stream the weights at HBM speed.
+//
+// Work: a workgroup owns one K range of 1024 elements and a strided list of
+// 16-row weight groups (gate and up rows are separate groups).  The range's
+// activations for all tokens (padded to a multiple of 16) go to LDS once,
+// 16-byte chunks XOR-swizzled by token so the MFMA operand reads of 16
+// tokens hit distinct banks.  Each wave streams its groups, two in flight:
+// lane l loads 16 bytes (one 32-element block) of row l % 16 at block
+// 4c + l / 16 of the range (c = 0..7), so one load instruction covers 16 rows
+// x 64 contiguous bytes and the lane's registers are already the A operand
+// of v_mfma_f32_16x16x32_bf16: k-group l / 16 of MFMA (c, quarter q) is block
+// 4c + l / 16, quarter q, for weights and activations alike.  The e8m0 bytes
+// of a lane's row come as two 16-byte loads (the range's 32 blocks); block
+// 4c + g's byte is byte g of dword c.  The fp32 partial tile goes to a
+// workspace [K range][token][matrix * R + row]; tile_reduce adds the ranges
+// in order (bit-reproducible) and applies SiLU * up, or the residual.
+#include <algorithm>
+#include <cstdlib>
+#include <type_traits>
+
+#include "mxfp4_common.hpp"
+#include "mxfp4_launch.hpp"
+
+namespace tinyinfer {
+
+namespace {
+
+constexpr int kTW = 8;                     // waves per workgroup
+constexpr int kTThreads = kTW * 64;
+constexpr int kRangeK = 1024;              // K elements per workgroup range
+constexpr int kRangeLoads = kRangeK / 128; // 16-byte loads per lane per group (16 rows x 64 B each)
+constexpr int kTokenLds = kRangeK * 2;     // LDS bytes per token of the range
+
+struct TileArgs {
+  const uint16_t* x;       // [M, K]
+  const uint8_t* w0;       // [R, K/2] gate (or down)
+  const uint8_t* s0;       // [R, K/32]
+  const uint8_t* w1;       // [R, K/2] up (gate_up only; else = w0)
+  const uint8_t* s1;
+  float* ws;               // [nkr][mpad][nmat * R] fp32 partials
+  int M, K, R;
+  int mpad;                // tokens padded to 16 * MT
+  int nmat;                // 2: gate_up, 1: down
+  int nkr;                 // K / 1024
+  int wpk;                 // workgroups per K range
+  int ngroups;             // nmat * R / 16
+  int nblk;                // K / 32
+};
+
+struct TileBuf {
+  u32x4_t w[kRangeLoads];
+  u32x4_t s[2];            // the row's 32 scale bytes of the range
+};
+
+// Loads of row group G for K range kr.  Scales first.
+__device__ __forceinline__ void tile_issue(const TileArgs& a, int G, int kr, TileBuf& b) {
+  const int lane = threadIdx.x & 63;
+  const int rg = a.R / 16;
+  const int m = G / rg;
+  const int64_t row = (int64_t)(G - m * rg) * 16 + (lane & 15);
+  const uint8_t* sp = (m ? a.s1 : a.s0) + row * a.nblk + kr * 32;
+  b.s[0] = *reinterpret_cast<const u32x4_t*>(sp);
+  b.s[1] = *reinterpret_cast<const u32x4_t*>(sp + 16);
+  const uint8_t* wp = (m ? a.w1 : a.w0) + row * (a.K / 2) + (int64_t)kr * (kRangeK / 2) + 16 * (lane >> 4);
+  // plain loads: the non-temporal hint measured slower for this pattern (8B
+  // down at 16 tokens 14.8 against 13.0 us, 64 tokens 26.6 against 22.1)
+#pragma unroll
+  for (int c = 0; c < kRangeLoads; ++c) b.w[c] = *reinterpret_cast<const u32x4_t*>(wp + 64 * c);
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+__device__ __forceinline__ uint32_t tile_scale(const TileBuf& b, int c) {
+  return (b.s[c >> 2][c & 3] >> (8 * ((threadIdx.x >> 4) & 3))) & 0xffu;
+}
+
+template <int MT, bool FAST>
+__device__ __forceinline__ void tile_mma(const TileBuf& b, const uint8_t* lds, f32x4_t (&acc)[MT]) {
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int c = 0; c < kRangeLoads; ++c) {
+    const uint32_t sb = tile_scale(b, c);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const u32x4_t wa = FAST ? dq8_bf16_fast(b.w[c][q], sb) : dq8_bf16_exact(b.w[c][q], sb);
+      const int ch = (4 * c + g) * 4 + q;   // 16-byte chunk of the range
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const u32x4_t xb = *reinterpret_cast<const u32x4_t*>(lds + (16 * mt + n) * kTokenLds + 16 * (ch ^ n));
+        acc[mt] = mfma16x16x32(wa, xb, acc[mt]);
+      }
+    }
+  }
+}
+
+template <int MT>
+__global__ __launch_bounds__(kTThreads, 1) void tile_kernel(TileArgs a) {
+  constexpr int kXPre = MT * 16 * (kRangeK / 8) / kTThreads;   // 16-byte x chunks per thread
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int kr = blockIdx.x % a.nkr;
+  const int wi = blockIdx.x / a.nkr;
+  const int nslots = a.wpk * kTW;
+  const int slot = wi * kTW + wave;
+  const int units = slot < a.ngroups ? (a.ngroups - slot + nslots - 1) / nslots : 0;
+
+  // the range's activations: token t = c / 128, chunk c % 128 (clamped rows
+  // past M are loaded and replaced by zeros)
+  u32x4_t xv[kXPre];
+#pragma unroll
+  for (int p = 0; p < kXPre; ++p) {
+    const int c = threadIdx.x + p * kTThreads;
+    const int t = c >> 7;
+    const int tr = t < a.M ? t : a.M - 1;
+    xv[p] = *reinterpret_cast<const u32x4_t*>(a.x + (int64_t)tr * a.K + (int64_t)kr * kRangeK + 8 * (c & 127));
+  }
+  TileBuf b0, b1;
+  auto group_of = [&](int j) { return units > 0 ? slot + (j < units ? j : units - 1) * nslots : slot % a.ngroups; };
+  tile_issue(a, group_of(0), kr, b0);
+  tile_issue(a, group_of(1), kr, b1);
+#pragma unroll
+  for (int p = 0; p < kXPre; ++p) {
+    const int c = threadIdx.x + p * kTThreads;
+    const int t = c >> 7;
+    const u32x4_t v = t < a.M ? xv[p] : u32x4_t{0u, 0u, 0u, 0u};
+    *reinterpret_cast<u32x4_t*>(lds + t * kTokenLds + 16 * ((c & 127) ^ (t & 15))) = v;
+  }
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);    // lgkmcnt(0): LDS only, not the weights in flight
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+
+  const int nmr = a.nmat * a.R;
+  auto step = [&](TileBuf& b, int j, auto issue_tag) {
+    const int G = group_of(j);
+    f32x4_t acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    bool ok = true;
+#pragma unroll
+    for (int c = 0; c < kRangeLoads; ++c) ok = ok && e8m0_fast_ok(tile_scale(b, c));
+    if (wave_all(ok)) tile_mma<MT, true>(b, lds, acc);
+    else tile_mma<MT, false>(b, lds, acc);
+    if constexpr (decltype(issue_tag)::value) tile_issue(a, group_of(j + 2), kr, b);
+    // lane l holds rows 4 (l / 16) + v of the group, token 16 mt + l % 16
+    const int rg = a.R / 16;
+    const int m = G / rg;
+    const int col = m * a.R + (G - m * rg) * 16 + 4 * (lane >> 4);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int t = 16 * mt + (lane & 15);
+      *reinterpret_cast<f32x4_t*>(a.ws + ((int64_t)kr * a.mpad + t) * nmr + col) = acc[mt];
+    }
+  };
+  constexpr std::true_type kIssue{};
+  constexpr std::false_type kLast{};
+  // every load issued is a group the wave multiplies (tails peeled; an issue
+  // under a condition inside the loop would drain the load queue each step)
+  int j = 0;
+  for (; j + 3 < units; j += 2) {
+    step(b0, j, kIssue);
+    step(b1, j + 1, kIssue);
+  }
+  const int left = units - j;
+  if (left == 3) {
+    step(b0, j, kIssue);
+    step(b1, j + 1, kLast);
+    step(b0, j + 2, kLast);
+  } else if (left == 2) {
+    step(b0, j, kLast);
+    step(b1, j + 1, kLast);
+  } else if (left == 1) {
+    step(b0, j, kLast);
+  }
+}
+
+// out[m][n] = epilogue(sum over kr of ws[kr][m][n] (and [R + n] for up)), in
+// kr order; four outputs per thread.
+template <int NMAT>
+__global__ __launch_bounds__(256) void tile_reduce(const float* __restrict__ ws, uint16_t* out, const uint16_t* res,
+                                                   int M, int mpad, int R, int nkr) {
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t total = (int64_t)M * R / 4;
+  if (q >= total) return;
+  const int64_t m = q / (R / 4);
+  const int n = (int)(q - m * (R / 4)) * 4;
+  // loads in batches of 8 ranges (issued together, then added in range order)
+  constexpr int kBatch = 8;
+  f32x4_t g = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
+  const int64_t stride = (int64_t)mpad * (NMAT * R);
+  const float* base = ws + m * (NMAT * R) + n;
+  for (int k0 = 0; k0 < nkr; k0 += kBatch) {
+    f32x4_t pg[kBatch], pu[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int kr = k0 + i < nkr ? k0 + i : nkr - 1;
+      pg[i] = *reinterpret_cast<const f32x4_t*>(base + kr * stride);
+      if constexpr (NMAT == 2) pu[i] = *reinterpret_cast<const f32x4_t*>(base + kr * stride + R);
+    }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      if (k0 + i < nkr) {
+        g += pg[i];
+        if constexpr (NMAT == 2) u += pu[i];
+      }
+    }
+  }
+  float v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = NMAT == 2 ? silu_f32(g[e]) * u[e] : g[e];
+  const uint32_t lo = (uint32_t)f32_to_act<kBF16>(v[0]) | ((uint32_t)f32_to_act<kBF16>(v[1]) << 16);
+  const uint32_t hi = (uint32_t)f32_to_act<kBF16>(v[2]) | ((uint32_t)f32_to_act<kBF16>(v[3]) << 16);
+  *reinterpret_cast<u32x2_t*>(out + m * R + n) = with_residual4<kBF16>(u32x2_t{lo, hi}, res, m * R + n);
+}
+
+int tile_cus() {
+  static int cache[64];
+  static bool init[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (!init[dev]) {
+    hipDeviceProp_t prop;
+    cache[dev] = hipGetDeviceProperties(&prop, dev) == hipSuccess ? prop.multiProcessorCount : 0;
+    init[dev] = true;
+  }
+  return cache[dev];
+}
+
+// Workgroups per K range: about one workgroup per CU over all ranges, at
+// least one group per wave.
+bool tile_plan(int64_t M, int64_t K, int64_t R, bool gateup, TileArgs& a, int& grid, int& mt, size_t& ws_bytes) {
+  const int cus = tile_cus();
+  if (cus < 1 || M < 1 || M > 64 || K < kRangeK || K % kRangeK != 0 || K > (1 << 20) || R < 16 || R % 16 != 0 ||
+      R > (1 << 22))
+    return false;
+  mt = (int)((M + 15) / 16);
+  a.M = (int)M;
+  a.K = (int)K;
+  a.R = (int)R;
+  a.mpad = 16 * mt;
+  a.nmat = gateup ? 2 : 1;
+  a.nkr = (int)(K / kRangeK);
+  a.ngroups = (int)(a.nmat * R / 16);
+  a.nblk = (int)(K / kBlock);
+  int wpk = std::max(1, cus / a.nkr);
+  wpk = std::min(wpk, (a.ngroups + kTW - 1) / kTW);
+  a.wpk = wpk;
+  grid = a.nkr * wpk;
+  ws_bytes = (size_t)a.nkr * a.mpad * a.nmat * (size_t)R * sizeof(float);
+  return true;
+}
+
+bool aligned_tile(const void* p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) & (n - 1)) == 0; }
+
+template <int MT>
+hipError_t tile_launch(const TileArgs& a, int grid, hipStream_t st) {
+  const int lds = MT * 16 * kTokenLds;
+  auto k = tile_kernel<MT>;
+  if (lds > 64 * 1024 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, lds) !=
+          hipSuccess)
+    return hipErrorNotSupported;
+  hipLaunchKernelGGL(k, dim3(grid), dim3(kTThreads), (size_t)lds, st, a);
+  return hipGetLastError();
+}
+
+template <bool GATEUP>
+hipError_t tile_stage(const MlpArgs& m, hipStream_t st) {
+  TileArgs a;
+  int grid = 0, mt = 0;
+  size_t bytes = 0;
+  const int64_t K = GATEUP ? m.hidden : m.inter;
+  const int64_t R = GATEUP ? m.inter : m.hidden;
+  if (m.dtype != kBF16 || !tile_plan(m.n, K, R, GATEUP, a, grid, mt, bytes)) return hipErrorNotSupported;
+  a.ws = gemm_split_workspace(bytes, st);
+  if (!a.ws) return hipErrorNotSupported;
+  a.x = static_cast<const uint16_t*>(GATEUP ? m.x : m.tmp);
+  a.w0 = GATEUP ? m.gate : m.down;
+  a.s0 = GATEUP ? m.gate_scale : m.down_scale;
+  a.w1 = GATEUP ? m.up : a.w0;
+  a.s1 = GATEUP ? m.up_scale : a.s0;
+  hipError_t e = hipErrorNotSupported;
+  switch (mt) {
+    case 1: e = tile_launch<1>(a, grid, st); break;
+    case 2: e = tile_launch<2>(a, grid, st); break;
+    case 3: e = tile_launch<3>(a, grid, st); break;
+    case 4: e = tile_launch<4>(a, grid, st); break;
+    default: break;
+  }
+  if (e != hipSuccess) return e;
+  uint16_t* out = static_cast<uint16_t*>(GATEUP ? m.tmp : m.out);
+  const uint16_t* res = GATEUP ? nullptr : static_cast<const uint16_t*>(m.residual);
+  const int64_t groups = m.n * R / 4;
+  tile_reduce<GATEUP ? 2 : 1><<<(unsigned)((groups + 255) / 256), 256, 0, st>>>(a.ws, out, res, a.M, a.mpad, a.R,
+                                                                                 a.nkr);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool tile_enabled() {
+  const char* e = std::getenv("TINYINFER_TILE");
+  return !(e && e[0] == '0' && e[1] == '\0');
+}
+
+bool tile_supported(const MlpArgs& m, int stage, hipStream_t st) {
+  if (m.dtype != kBF16) return false;
+  if ((stage & kStageGateUp) && m.norm_w != nullptr) return false;
+  TileArgs a;
+  int grid = 0, mt = 0;
+  size_t bytes = 0, need = 0;
+  if (stage & kStageGateUp) {
+    if (!tile_plan(m.n, m.hidden, m.inter, true, a, grid, mt, bytes)) return false;
+    need = std::max(need, bytes);
+  }
+  if (stage & kStageDown) {
+    if (!tile_plan(m.n, m.inter, m.hidden, false, a, grid, mt, bytes)) return false;
+    need = std::max(need, bytes);
+  }
+  // 16-byte loads of activations, weights and scale runs; 8-byte output stores
+  const void* p16[] = {m.x, m.gate, m.up, m.down, m.gate_scale, m.up_scale, m.down_scale, m.tmp};
+  for (const void* p : p16)
+    if (p && !aligned_tile(p, 16)) return false;
+  const void* p8[] = {m.out, m.residual};
+  for (const void* p : p8)
+    if (p && !aligned_tile(p, 8)) return false;
+  return gemm_split_workspace(need, st) != nullptr;
+}
+
+hipError_t launch_tile_mlp(const MlpArgs& m, int stage, hipStream_t st) {
+  if (stage & kStageGateUp) {
+    const hipError_t e = tile_stage<true>(m, st);
+    if (e != hipSuccess) return e;
+  }
+  if (stage & kStageDown) return tile_stage<false>(m, st);
+  return hipSuccess;
+}
+
+}  // namespace tinyinfer
