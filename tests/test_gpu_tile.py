@@ -95,9 +95,9 @@ def test_tile_full_call_residual(capi, m):
 
 
 def test_tile_dispatch_and_switch(capi):
-    """AUTO runs the tile kernels (two launches per stage) for 16 tokens at
-    the 8B shape; TINYINFER_TILE=0 sends the call to the GEMM path, and both
-    agree within the parity bar."""
+    """AUTO runs the tile kernels for 16 tokens at the 8B shape (gate_up in one
+    launch, down as tile kernel + reduce); TINYINFER_TILE=0 sends the call to
+    the GEMM path, and both agree within the parity bar."""
     banner("tile dispatch")
     x, mats = make_case(16, 4096, 12288, seed=600)
     xd, md = to_dev(x, mats)
@@ -113,6 +113,35 @@ def test_tile_dispatch_and_switch(capi):
     check_close(out["0"].cpu(), ref, "GEMM path")
     if not names["1"]:
         pytest.skip("the profiler recorded no kernels here; parity checked, dispatch not")
-    assert sum("tile_kernel" in n for n in names["1"]) == 2, names["1"]
-    assert sum("tile_reduce" in n for n in names["1"]) == 2, names["1"]
-    assert not any("tile_kernel" in n for n in names["0"]), names["0"]
+    assert sum("tile_gu_kernel" in n for n in names["1"]) == 1, names["1"]
+    assert sum("tile_kernel" in n for n in names["1"]) == 1, names["1"]
+    assert sum("tile_reduce" in n for n in names["1"]) == 1, names["1"]
+    assert not any("tile_kernel" in n or "tile_gu_kernel" in n for n in names["0"]), names["0"]
+
+
+@pytest.mark.parametrize("m,h,i", [
+    (9, 4096, 12288), (16, 4096, 12288),   # four K ranges, one block per workgroup iteration
+    (24, 2048, 6144), (32, 2048, 6144),    # two ranges, two column tiles
+    (20, 1024, 3072),                      # one range, four blocks per iteration
+])
+def test_tile_gate_up_in_one_launch(capi, m, h, i):
+    """gate_up with all of x in LDS runs as one launch that adds the K ranges'
+    partial tiles in LDS: bit-identical to the split kernel + reduce (the same
+    partials added in the same order; TINYINFER_TILE_GU=0), and one kernel
+    instead of two."""
+    banner(f"tile gate_up one launch m={m} h={h} i={i}")
+    x, mats = make_case(m, h, i, seed=900 + m + h)
+    xd, md = to_dev(x, mats)
+    out, names = {}, {}
+    for flag in ("1", "0"):
+        os.environ["TINYINFER_TILE_GU"] = flag
+        try:
+            names[flag] = kernel_names(lambda: out.__setitem__(flag, capi.gate_up(xd, *md[:4], path=SKINNY)))
+        finally:
+            del os.environ["TINYINFER_TILE_GU"]
+    assert torch.equal(out["1"].view(torch.int16), out["0"].view(torch.int16))
+    check_close(out["1"].cpu(), h_semantics(x, *mats[:4]), f"m={m} gate_up")
+    if names["1"]:
+        assert sum("tile_gu_kernel" in n for n in names["1"]) == 1, names["1"]
+        assert not any("tile_reduce" in n for n in names["1"]), names["1"]
+        assert sum("tile_reduce" in n for n in names["0"]) == 1, names["0"]

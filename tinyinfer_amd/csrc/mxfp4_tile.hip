@@ -77,8 +77,9 @@ __device__ __forceinline__ uint32_t tile_scale(const TileBuf& b, int c) {
   return (b.s[c >> 2][c & 3] >> (8 * ((threadIdx.x >> 4) & 3))) & 0xffu;
 }
 
+// lds: the K range's activations, token t at lds + t * tstride
 template <int MT, bool FAST>
-__device__ __forceinline__ void tile_mma(const TileBuf& b, const uint8_t* lds, f32x4_t (&acc)[MT]) {
+__device__ __forceinline__ void tile_mma(const TileBuf& b, const uint8_t* lds, int tstride, f32x4_t (&acc)[MT]) {
   const int lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
 #pragma unroll
@@ -90,7 +91,7 @@ __device__ __forceinline__ void tile_mma(const TileBuf& b, const uint8_t* lds, f
       const int ch = (4 * c + g) * 4 + q;   // 16-byte chunk of the range
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const u32x4_t xb = *reinterpret_cast<const u32x4_t*>(lds + (16 * mt + n) * kTokenLds + 16 * (ch ^ n));
+        const u32x4_t xb = *reinterpret_cast<const u32x4_t*>(lds + (16 * mt + n) * tstride + 16 * (ch ^ n));
         acc[mt] = mfma16x16x32(wa, xb, acc[mt]);
       }
     }
@@ -144,8 +145,8 @@ __global__ __launch_bounds__(kTThreads, 1) void tile_kernel(TileArgs a) {
     bool ok = true;
 #pragma unroll
     for (int c = 0; c < kRangeLoads; ++c) ok = ok && e8m0_fast_ok(tile_scale(b, c));
-    if (wave_all(ok)) tile_mma<MT, true>(b, lds, acc);
-    else tile_mma<MT, false>(b, lds, acc);
+    if (wave_all(ok)) tile_mma<MT, true>(b, lds, kTokenLds, acc);
+    else tile_mma<MT, false>(b, lds, kTokenLds, acc);
     if constexpr (decltype(issue_tag)::value) tile_issue(a, group_of(j + 2), kr, b);
     // lane l holds rows 4 (l / 16) + v of the group, token 16 mt + l % 16
     const int rg = a.R / 16;
@@ -218,6 +219,119 @@ __global__ __launch_bounds__(256) void tile_reduce(const float* __restrict__ ws,
   *reinterpret_cast<u32x2_t*>(out + m * R + n) = with_residual4<kBF16>(u32x2_t{lo, hi}, res, m * R + n);
 }
 
+// gate_up without the K split, when all of x fits LDS (S = K / 1024 ranges,
+// MT * S <= 4): a workgroup iteration takes 4 / S blocks of 16 gate rows and
+// the 16 matching up rows; wave w multiplies matrix (w / S) % 2 of block
+// w / (2 S) over K range w % S.  The partial tiles meet in LDS (two buffers,
+// so one barrier per iteration), and the workgroup adds each output's ranges
+// in order, applies SiLU * up and stores h: no workspace round trip and no
+// reduce launch.  Every wave runs the same iterations (the barrier); blocks
+// past the end repeat the last one and store to `dummy` instead.
+template <int MT, int S>
+__global__ __launch_bounds__(kTThreads, 1) void tile_gu_kernel(TileArgs a, uint16_t* out, uint16_t* dummy) {
+  static_assert(S == 1 || S == 2 || S == 4, "8 waves = (4 / S) blocks x 2 matrices x S ranges");
+  constexpr int kBlocks = 4 / S;
+  constexpr int kMpad = 16 * MT;
+  constexpr int kXPre = kMpad * S * (kRangeK / 8) / kTThreads;
+  constexpr int kOut = kBlocks * 16 * kMpad;                  // outputs per iteration
+  constexpr int kOutTrips = kOut >= kTThreads ? kOut / kTThreads : 1;
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int tstride = S * kRangeK * 2;                         // LDS bytes per token (all of K)
+  float* part = reinterpret_cast<float*>(lds + kMpad * tstride);   // [2][8 waves][MT][64 lanes][4]
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int rbl = wave / (2 * S), mat = (wave / S) & 1, sp = wave % S;
+  const int nrb = a.R / 16;
+  const int per_iter = (int)gridDim.x * kBlocks;
+  const int niter = (nrb + per_iter - 1) / per_iter;
+  auto rb_of = [&](int it) {
+    const int rb = (it * (int)gridDim.x + (int)blockIdx.x) * kBlocks + rbl;
+    return rb < nrb ? rb : nrb - 1;
+  };
+
+  // all of x: token t = c / (K / 8), 16-byte chunk c % (K / 8); per K range
+  // the split kernel's swizzle
+  const int nxr = a.K / 8;
+  u32x4_t xv[kXPre];
+#pragma unroll
+  for (int p = 0; p < kXPre; ++p) {
+    const int c = threadIdx.x + p * kTThreads;
+    const int t = c / nxr;
+    const int tr = t < a.M ? t : a.M - 1;
+    xv[p] = *reinterpret_cast<const u32x4_t*>(a.x + (int64_t)tr * a.K + 8 * (c - t * nxr));
+  }
+  TileBuf b0, b1;
+  tile_issue(a, mat * nrb + rb_of(0), sp, b0);
+  tile_issue(a, mat * nrb + rb_of(1), sp, b1);
+#pragma unroll
+  for (int p = 0; p < kXPre; ++p) {
+    const int c = threadIdx.x + p * kTThreads;
+    const int t = c / nxr, cc = c - t * nxr;
+    const u32x4_t v = t < a.M ? xv[p] : u32x4_t{0u, 0u, 0u, 0u};
+    *reinterpret_cast<u32x4_t*>(lds + t * tstride + (cc >> 7) * kTokenLds + 16 * ((cc & 127) ^ (t & 15))) = v;
+  }
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);    // lgkmcnt(0): LDS only, not the weights in flight
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+
+  auto step = [&](TileBuf& b, int it, auto issue_tag) {
+    f32x4_t acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    bool ok = true;
+#pragma unroll
+    for (int c = 0; c < kRangeLoads; ++c) ok = ok && e8m0_fast_ok(tile_scale(b, c));
+    if (wave_all(ok)) tile_mma<MT, true>(b, lds + sp * kTokenLds, tstride, acc);
+    else tile_mma<MT, false>(b, lds + sp * kTokenLds, tstride, acc);
+    if constexpr (decltype(issue_tag)::value) tile_issue(a, mat * nrb + rb_of(it + 2), sp, b);
+    float* pw = part + ((it & 1) * kTW + wave) * MT * 256;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) *reinterpret_cast<f32x4_t*>(pw + (mt * 64 + lane) * 4) = acc[mt];
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    // outputs o = (block, token, row): row fastest, so a token's 16 rows are
+    // one 32-byte store run
+    const float* pr = part + (it & 1) * kTW * MT * 256;
+#pragma unroll
+    for (int k = 0; k < kOutTrips; ++k) {
+      const int o = kOut >= kTThreads ? (int)threadIdx.x + k * kTThreads : (int)threadIdx.x % kOut;
+      const int i = o & 15, t = (o >> 4) % kMpad, bl = (o >> 4) / kMpad;
+      const int ln = 16 * (i >> 2) + (t & 15), v = i & 3, mt = t >> 4;
+      float g = 0.f, u = 0.f;
+#pragma unroll
+      for (int s2 = 0; s2 < S; ++s2) {
+        g += pr[(((bl * 2 * S + s2) * MT + mt) * 64 + ln) * 4 + v];
+        u += pr[(((bl * 2 * S + S + s2) * MT + mt) * 64 + ln) * 4 + v];
+      }
+      const int rb = (it * (int)gridDim.x + (int)blockIdx.x) * kBlocks + bl;
+      const bool valid = rb < nrb && t < a.M && (kOut >= kTThreads || (int)threadIdx.x < kOut);
+      uint16_t* dst = valid ? out + (int64_t)t * a.R + rb * 16 + i : dummy + threadIdx.x;
+      *dst = f32_to_act<kBF16>(silu_f32(g) * u);
+    }
+  };
+  constexpr std::true_type kIssue{};
+  constexpr std::false_type kLast{};
+  int it = 0;
+  for (; it + 3 < niter; it += 2) {
+    step(b0, it, kIssue);
+    step(b1, it + 1, kIssue);
+  }
+  const int left = niter - it;
+  if (left == 3) {
+    step(b0, it, kIssue);
+    step(b1, it + 1, kLast);
+    step(b0, it + 2, kLast);
+  } else if (left == 2) {
+    step(b0, it, kLast);
+    step(b1, it + 1, kLast);
+  } else if (left == 1) {
+    step(b0, it, kLast);
+  }
+}
+
 int tile_cus() {
   static int cache[64];
   static bool init[64] = {};
@@ -269,6 +383,31 @@ hipError_t tile_launch(const TileArgs& a, int grid, hipStream_t st) {
   return hipGetLastError();
 }
 
+// gate_up in one launch (tile_gu_kernel): S = K / 1024 ranges in {1, 2, 4},
+// at most two column tiles, all of x plus the partial buffers within LDS.
+bool tile_gu_fits(const TileArgs& a, int mt) {
+  const int S = a.nkr;
+  return (S == 1 || S == 2 || S == 4) && mt <= 2 && mt * S <= 4 && a.R % 16 == 0;
+}
+
+bool tile_gu_enabled() {
+  const char* e = std::getenv("TINYINFER_TILE_GU");
+  return !(e && e[0] == '0' && e[1] == '\0');
+}
+
+template <int MT, int S>
+hipError_t tile_gu_launch(const TileArgs& a, int grid, uint16_t* out, hipStream_t st) {
+  const int lds = 16 * MT * S * kTokenLds + 2 * kTW * MT * 256 * (int)sizeof(float);
+  auto k = tile_gu_kernel<MT, S>;
+  if (lds > 64 * 1024 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, lds) !=
+          hipSuccess)
+    return hipErrorNotSupported;
+  // stores of outputs past the end go to the (otherwise unused) workspace
+  hipLaunchKernelGGL(k, dim3(grid), dim3(kTThreads), (size_t)lds, st, a, out, reinterpret_cast<uint16_t*>(a.ws));
+  return hipGetLastError();
+}
+
 template <bool GATEUP>
 hipError_t tile_stage(const MlpArgs& m, hipStream_t st) {
   TileArgs a;
@@ -284,6 +423,22 @@ hipError_t tile_stage(const MlpArgs& m, hipStream_t st) {
   a.s0 = GATEUP ? m.gate_scale : m.down_scale;
   a.w1 = GATEUP ? m.up : a.w0;
   a.s1 = GATEUP ? m.up_scale : a.s0;
+  if constexpr (GATEUP) {
+    if (tile_gu_fits(a, mt) && tile_gu_enabled()) {
+      const int S = a.nkr;
+      const int kblocks = 4 / S;
+      const int nrb = a.R / 16;
+      const int g2 = std::min(tile_cus(), (nrb + kblocks - 1) / kblocks);
+      switch (mt * 8 + S) {
+        case 8 + 1: return tile_gu_launch<1, 1>(a, g2, static_cast<uint16_t*>(m.tmp), st);
+        case 8 + 2: return tile_gu_launch<1, 2>(a, g2, static_cast<uint16_t*>(m.tmp), st);
+        case 8 + 4: return tile_gu_launch<1, 4>(a, g2, static_cast<uint16_t*>(m.tmp), st);
+        case 16 + 1: return tile_gu_launch<2, 1>(a, g2, static_cast<uint16_t*>(m.tmp), st);
+        case 16 + 2: return tile_gu_launch<2, 2>(a, g2, static_cast<uint16_t*>(m.tmp), st);
+        default: break;
+      }
+    }
+  }
   hipError_t e = hipErrorNotSupported;
   switch (mt) {
     case 1: e = tile_launch<1>(a, grid, st); break;
