@@ -72,10 +72,11 @@ bool rowpair_enabled();
 bool rowpair_supported(const MlpArgs& a, int stage);
 hipError_t launch_rowpair_mlp(const MlpArgs& a, int stage, hipStream_t stream);
 
-// Split-K tile kernels for 5..64 tokens (bf16, K % 1024 == 0): a workgroup
+// Split-K tile kernels for up to 64 tokens (bf16, K % 1024 == 0): a workgroup
 // owns one 1024-element K range (its activations staged once in LDS) and
 // streams 16-row weight groups through MFMA; a reduce launch adds the K
-// ranges in order and applies the epilogue.  tile_supported() says whether
+// ranges in order and applies the epilogue (gate_up in one launch, partials
+// added in LDS, when all of x fits).  tile_supported() says whether
 // the call fits and its fp32 workspace can be had (not during graph capture
 // unless the stream's workspace is already large enough); tile_enabled() is
 // false when TINYINFER_TILE=0.

@@ -1,7 +1,8 @@
-// Split-K tile kernels for small batches (5..64 bf16 tokens): the reference's
-// per-token GEMV stages mlp_stage1_mxfp4 / mlp_stage2_mxfp4
+// Split-K tile kernels for small batches (up to 64 bf16 tokens): the
+// reference's per-token GEMV stages mlp_stage1_mxfp4 / mlp_stage2_mxfp4
 // (tinyinfer/csrc/mlp_fp4.cu:79-142, 365-426) for a batch whose activations
-// are too many for the decode kernels' registers and too few for the
+// are too many for the decode kernels' registers (or whose K they decline,
+// e.g. a 25600-element down stage beyond two tokens) and too few for the
 // prefill GEMM's 64-token tiles to stream the weights at HBM speed.
 //
 // Work: a workgroup owns one K range of 1024 elements and a strided list of
