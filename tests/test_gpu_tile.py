@@ -145,3 +145,50 @@ def test_tile_gate_up_in_one_launch(capi, m, h, i):
         assert sum("tile_gu_kernel" in n for n in names["1"]) == 1, names["1"]
         assert not any("tile_reduce" in n for n in names["1"]), names["1"]
         assert sum("tile_reduce" in n for n in names["0"]) == 1, names["0"]
+
+
+@pytest.mark.parametrize("m", [16, 40])
+def test_tile_graph_replays(capi, m):
+    """Graphs: on a capture stream that already ran the call eagerly (so its
+    workspace exists) the tile kernels are captured, and every replay, with
+    eager work between replays, gives the eager bits (16 tokens: one-launch
+    gate_up + down with its reduce; 40: both stages split + reduce). On a
+    fresh capture stream the workspace cannot be allocated: the call is
+    captured on another kernel family, still within tolerance."""
+    banner(f"tile graph replays m={m}")
+    x, mats = make_case(m, 4096, 12288, seed=700 + m)
+    xd, md = to_dev(x, mats)
+    ref = om.mlp_kernel_semantics(x, *mats)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    out = torch.empty((m, 4096), dtype=torch.bfloat16, device="cuda")
+    tmp = torch.empty((m, 12288), dtype=torch.bfloat16, device="cuda")
+    with torch.cuda.stream(s):
+        capi.mlp_forward(xd, *md, out=out, tmp=tmp, path=AUTO)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    eager = out.clone()
+    check_close(eager.cpu(), ref, "eager tile")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for _ in range(2):
+            capi.mlp_forward(xd, *md, out=out, tmp=tmp, path=AUTO)
+    for _ in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), eager.view(torch.int16))
+        capi.mlp_forward(xd, *md, path=AUTO)          # eager work between replays
+        torch.cuda.synchronize()
+    del g
+    g2 = torch.cuda.CUDAGraph()
+    out2 = torch.empty_like(out)
+    with torch.cuda.graph(g2):                        # a fresh capture stream
+        capi.mlp_forward(xd, *md, out=out2, tmp=tmp, path=AUTO)
+    for _ in range(2):
+        out2.zero_()
+        torch.cuda.synchronize()
+        g2.replay()
+        torch.cuda.synchronize()
+        check_close(out2.cpu(), ref, "fresh-stream capture")
