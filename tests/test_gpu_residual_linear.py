@@ -37,6 +37,8 @@ def _added(res, y):
     (4, 2048, 6144, AUTO, torch.float16),         # stream kernels, fp16
     (2, 1024, 3072, DECODE, torch.bfloat16),      # fused decode kernel
     (24, 1024, 1536, SKINNY, torch.bfloat16),     # skinny kernels
+    (16, 1024, 3072, AUTO, torch.bfloat16),       # tile kernels: one-launch gate_up, down + reduce
+    (40, 2048, 6144, SKINNY, torch.bfloat16),     # tile kernels: both stages split + reduce
     (300, 1024, 1536, GEMM, torch.bfloat16),      # ring GEMM, unsplit down
     (160, 2048, 6144, GEMM, torch.bfloat16),      # ring GEMM, split-K down + reduce
     (130, 1024, 1536, GEMM, torch.float16),       # register-staged GEMM (fp16)
@@ -72,7 +74,7 @@ def test_residual_torch_extension(capi):
 
 
 @pytest.mark.parametrize("m,k,r", [(1, 4096, 6144), (7, 4096, 4096), (200, 2048, 2048), (3, 1024, 151936),
-                                   (96, 1536, 512)])
+                                   (96, 1536, 512), (16, 4096, 4096), (48, 2048, 2048)])
 def test_linear_against_exact_sums(capi, m, k, r):
     banner(f"linear m={m} k={k} r={r}")
     g = torch.Generator().manual_seed(k + r)
