@@ -348,7 +348,9 @@ int tile_cus() {
 }
 
 // Workgroups per K range: about one workgroup per CU over all ranges, at
-// least one group per wave.
+// least one group per wave, then as few as give every wave the same largest
+// number of groups (8B down at 16 tokens: 16 instead of 21 per range, two
+// groups per wave; 12.4 -> 12.1 us).
 bool tile_plan(int64_t M, int64_t K, int64_t R, bool gateup, TileArgs& a, int& grid, int& mt, size_t& ws_bytes) {
   const int cus = tile_cus();
   if (cus < 1 || M < 1 || M > 64 || K < kRangeK || K % kRangeK != 0 || K > (1 << 20) || R < 16 || R % 16 != 0 ||
@@ -365,6 +367,8 @@ bool tile_plan(int64_t M, int64_t K, int64_t R, bool gateup, TileArgs& a, int& g
   a.nblk = (int)(K / kBlock);
   int wpk = std::max(1, cus / a.nkr);
   wpk = std::min(wpk, (a.ngroups + kTW - 1) / kTW);
+  const int umax = (a.ngroups + wpk * kTW - 1) / (wpk * kTW);
+  wpk = (a.ngroups + umax * kTW - 1) / (umax * kTW);
   a.wpk = wpk;
   grid = a.nkr * wpk;
   ws_bytes = (size_t)a.nkr * a.mpad * a.nmat * (size_t)R * sizeof(float);
