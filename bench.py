@@ -1,6 +1,6 @@
 """Benchmark of the MXFP4 weight-only Qwen3 MLP on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--all]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
 
 Headline workload (BASELINE.json metric): the Qwen3-8B-shaped MLP
 (hidden 4096, intermediate 12288) at M=1 decode, reported as algorithmic HBM
@@ -10,14 +10,22 @@ batch of seeded synthetic activations, with the weight set rotated every step
 over enough independently seeded sets (>= 2 x 256 MiB) that the 256 MB
 Infinity Cache cannot hold them: every step streams its weights from HBM.
 
-Timing: W untimed warm-up steps, then exactly K steps captured in one HIP
-graph and replayed once between two device synchronizations (the graph keeps
-host launch overhead out of the M=1 number); HIP events on the stream the
-kernels run on (torch's current stream, which the C ABI is handed) bracket
-the replay.  The dominant kernel (the gate_up stage) is timed the same way
-on its own for the ``roofline`` object.  ``cpu_baseline`` times the CPU
-restatement of the reference's torch dequant-then-matmul path (the oracle)
-on a bounded sample of the same workload on this host.
+Timing: W untimed warm-up steps, then a HIP graph of exactly K steps is
+replayed R = max(10, ceil(200 / K)) times, each replay bracketed by HIP
+events on the stream the kernels run on (torch's current stream, which the C
+ABI is handed) and by device synchronizations.  Per-step time of a replay =
+its event time / K; ``ms_per_step`` and ``value`` come from the median over
+the R replays (>= 200 timed MLP calls), ``us_per_step_p10_p50_p90`` from the
+same replays.  The dominant kernel (the gate_up stage) is timed the same way
+on its own for the ``roofline`` object, at M=1 and at M=2048.
+
+``points`` holds the other BASELINE configurations, each timed the same way
+with its own rotated weight sets: Qwen3-1.7B at M=1/4/8, Qwen3-8B at
+M=16/64/256/512, and the Qwen3-32B 64-layer stack at M=1/512.
+``cpu_baseline`` times the CPU restatement of the reference's torch
+dequant-then-matmul path (the oracle) on this host: the whole call at 8B
+M=1 and M=2048 (per-call dequant + matmul, and matmul only), and per other
+configuration the dequant and the matmul-only parts.
 
 Work per MLP call:  bytes = 3*H*I*(1/2 + 1/32) + 4*M*H,  flops = 6*M*H*I.
 Prints one JSON line.
@@ -41,6 +49,8 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
 MALL_BYTES = 256 * 2 ** 20     # Infinity Cache
 PROFILE_DIR = os.path.join(ROOT, "profiles")
+MIN_TIMED_CALLS = 200          # timed MLP calls per reported figure
+MIN_REPLAYS = 10
 
 METRIC = "MXFP4 MLP GB/s (M=1) & TFLOP/s (M=2048), Qwen3-8B shape, % of peak"
 NORM_EPS = 1e-6                # Qwen3's rms_norm_eps
@@ -49,20 +59,18 @@ NORM_EPS = 1e-6                # Qwen3's rms_norm_eps
 def parse():
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=1000, help="timed M=1 steps (one MLP call each)")
-    p.add_argument("--warmup", type=int, default=50)
+    p.add_argument("--steps", type=int, default=100, help="MLP calls per timed graph replay")
+    p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--config", default="qwen3-8b")
     p.add_argument("--m", type=int, default=1, help="headline token count")
     p.add_argument("--prefill-m", type=int, default=2048, help="prefill token count (0: skip)")
-    p.add_argument("--prefill-steps", type=int, default=100)
-    p.add_argument("--all", action="store_true",
-                   help="also measure every other BASELINE config (1.7B decode, 8B M=256/512, 32B 64-layer stack) "
-                        "and 8B small batches (M=16, 64)")
+    p.add_argument("--quick", action="store_true", help="headline, roofline and prefill only (no points)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    p.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline sample budget")
+    p.add_argument("--cpu-seconds", type=float, default=30.0, help="CPU baseline budget (whole run)")
     p.add_argument("--copy-probe", action="store_true",
                    help="only run a 256 MiB device copy (calibrates rocprof FETCH/WRITE_SIZE)")
-    p.add_argument("--only", choices=["decode", "gate_up", "down", "prefill", "norm_mlp"], default=None,
+    p.add_argument("--only", choices=["decode", "gate_up", "down", "prefill", "prefill_gate_up", "prefill_down",
+                                      "norm_mlp"], default=None,
                    help="run a single timed loop (for rocprofv3 runs)")
     p.add_argument("--path", type=int, default=0,
                    help="kernel path for --only runs (0 auto, 1 skinny/stream, 2 GEMM, 3 fused decode)")
@@ -75,14 +83,24 @@ def log(msg: str) -> None:
 
 # ----------------------------------------------------------------- inputs
 
-def weight_sets(shape, min_bytes=2 * MALL_BYTES):
+def weight_sets(shape, min_bytes=2 * MALL_BYTES, generator="cpu"):
     """Independently seeded quantized weight sets whose total exceeds
-    ``min_bytes`` (layer index = set index -> seeds 1000+3*set+{0,1,2})."""
+    ``min_bytes`` (set s uses the seeds of layer s: 1000+3*s+{0,1,2}), drawn
+    with torch's CPU generator as BASELINE specifies, quantized on the GPU."""
     from tinyinfer_amd.workloads import quantized_weights, weight_bytes
     per = weight_bytes(shape.hidden, shape.inter)
     n = max(1, math.ceil(min_bytes / per))
-    sets = [quantized_weights(shape.hidden, shape.inter, layer=s, generator="cuda") for s in range(n)]
-    return sets
+    return [quantized_weights(shape.hidden, shape.inter, layer=s, generator=generator) for s in range(n)]
+
+
+def quantiles(v):
+    s = sorted(v)
+    pick = lambda q: s[min(len(s) - 1, int(round(q * (len(s) - 1))))]
+    return pick(0.1), pick(0.5), pick(0.9)
+
+
+def replays_for(steps: int) -> int:
+    return max(MIN_REPLAYS, math.ceil(MIN_TIMED_CALLS / max(1, steps)))
 
 
 class Runner:
@@ -115,6 +133,12 @@ class Runner:
         else:
             c.down(self.tmp, *w[4:], out=self.out, path=self.path)
 
+    def warm(self, n):
+        import torch
+        for s in range(n):
+            self.step(s)
+        torch.cuda.synchronize()
+
     def graph(self, steps):
         import torch
         g = torch.cuda.CUDAGraph()
@@ -132,13 +156,17 @@ class Runner:
         torch.cuda.synchronize()
         return g
 
-    def time_graph(self, steps, reps=1):
-        """Per-step milliseconds of `reps` replays of a `steps`-call graph."""
+    def time_graph(self, steps, reps=None):
+        """Per-step milliseconds of each of `reps` timed replays of one
+        `steps`-call graph (after one untimed replay), and the wall time of
+        the timed replays."""
         import torch
+        reps = reps or replays_for(steps)
         g = self.graph(steps)
         g.replay()                            # warm replay
         torch.cuda.synchronize()
         per = []
+        t0 = time.perf_counter()
         for _ in range(reps):
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             torch.cuda.synchronize()
@@ -147,16 +175,15 @@ class Runner:
             b.record()
             torch.cuda.synchronize()
             per.append(a.elapsed_time(b) / steps)
+        wall = time.perf_counter() - t0
         del g
-        return per
+        return per, wall
 
 
 def eager_call_us(runner, calls=200):
     """Python-call wall time per MLP call (eager, incl. host overhead)."""
     import torch
-    for s in range(20):
-        runner.step(s)
-    torch.cuda.synchronize()
+    runner.warm(20)
     t0 = time.perf_counter()
     for s in range(calls):
         runner.step(s)
@@ -166,102 +193,166 @@ def eager_call_us(runner, calls=200):
 
 # ----------------------------------------------------------------- CPU baseline
 
-def cpu_baseline(shape, m, budget_s):
-    """The oracle's restatement of the reference torch CPU path, timed on a
-    bounded sample: per-call dequant + F.linear x3 (bf16) at the headline
-    shape and M, repeated until ``budget_s`` of CPU work."""
-    import torch
-    from oracle import mlp as om
-    from tinyinfer_amd.workloads import activations, alg_bytes, random_weights
-    from oracle import mxfp4 as ox
-
-    mats = []
-    for w in random_weights(shape.hidden, shape.inter, layer=0, generator="cpu"):
-        mats.extend(ox.quantize_chunk(w))
-    x = activations(m, shape.hidden, device="cpu")
-    om.mlp_reference(x, *mats)                       # warm-up
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while len(times) < 2 or (time.perf_counter() < t_end and len(times) < 50):
-        t0 = time.perf_counter()
-        om.mlp_reference(x, *mats)
-        times.append(time.perf_counter() - t0)
-        if len(times) >= 2 and time.perf_counter() > t_end:
-            break
-    t = statistics.median(times)
-    # matmul-only variant (pre-dequantized bf16 weights)
-    wts = tuple(om.dequant_weight(mats[2 * j], mats[2 * j + 1], x.dtype) for j in range(3))
-    om.mlp_reference(x, *mats, weights=wts)
-    mm = []
-    for _ in range(5):
-        t0 = time.perf_counter()
-        om.mlp_reference(x, *mats, weights=wts)
-        mm.append(time.perf_counter() - t0)
-    t_mm = statistics.median(mm)
-    b = alg_bytes(m, shape.hidden, shape.inter)
-    model = ""
+def _cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
                 if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
+                    return line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return {
-        "value": round(b / t / 1e9, 3),
-        "unit": "GB/s",
-        "cores": torch.get_num_threads(),
-        "kind": "port",
-        "sample": (f"{len(times)} calls of the torch CPU dequant-then-matmul path at {shape.name} "
-                   f"M={m} (median {t * 1e3:.1f} ms/call); matmul-only with pre-dequantized bf16 weights "
-                   f"{t_mm * 1e3:.1f} ms/call = {b / t_mm / 1e9:.3f} GB/s"),
-        "ms_per_call": round(t * 1e3, 3),
-        "matmul_only_gbs": round(b / t_mm / 1e9, 3),
-        "os_cpu_count": os.cpu_count(),
-        "cpu_model": model,
-    }
+    return ""
 
 
-# ----------------------------------------------------------------- traffic
+def _timed(fn, runs, budget_s):
+    """Median seconds of ``fn`` after one warm-up: ``runs`` runs, fewer (at
+    least two) when the budget runs out."""
+    fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < runs:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 2 and time.perf_counter() > t_end:
+            break
+    return statistics.median(times), len(times)
+
+
+def cpu_baseline(budget_s, quick):
+    """The oracle's restatement of the reference torch CPU path (weights
+    decoded with torch ops to fp32 then bf16, three F.linear calls,
+    SiLU*up) on this host's cores.  Whole calls at the headline shape (8B)
+    at M=1 and M=2048: (i) per-call dequant + matmul, (ii) matmul only on
+    pre-dequantized bf16 weights.  For the other configurations the two
+    parts are timed separately (the dequant once per shape, the matmul per
+    M) and (i) is their sum; for the 32B stack the dequant is timed on a
+    quarter of one layer's rows and the matmul on one whole layer, both
+    scaled to 64 layers.  The packed weights are the GPU runs' own (same
+    seeds), copied to the host; only the CPU work is timed."""
+    import torch
+    from oracle import mlp as om
+    from tinyinfer_amd.workloads import SHAPES, activations, alg_bytes, alg_flops, quantized_weights
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    t_start = time.perf_counter()
+
+    def mats_for(shp, generator):
+        return [a.cpu() for a in quantized_weights(shp.hidden, shp.inter, layer=0, generator=generator)]
+
+    def dequant_all(mats, rows=None):
+        return tuple(om.dequant_weight(mats[2 * j][:rows], mats[2 * j + 1][:rows], torch.bfloat16, "torch")
+                     for j in range(3))
+
+    res = {"unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
+           "os_cpu_count": os.cpu_count(), "cpu_model": _cpu_model()}
+    h8 = SHAPES["qwen3-8b"]
+    mats8 = mats_for(h8, "cpu")
+    whole = {}
+    for m in (1, 2048):
+        x = activations(m, h8.hidden, device="cpu")
+        t_i, n_i = _timed(lambda: om.mlp_reference(x, *mats8, impl="torch"), 5, budget_s * 0.15)
+        wts = dequant_all(mats8)
+        t_ii, n_ii = _timed(lambda: om.mlp_reference(x, *mats8, weights=wts), 5, budget_s * 0.1)
+        b, f = alg_bytes(m, h8.hidden, h8.inter), alg_flops(m, h8.hidden, h8.inter)
+        whole[m] = {"config": h8.name, "m": m, "ms_per_call": round(t_i * 1e3, 3), "runs": n_i,
+                    "gbs": round(b / t_i / 1e9, 3), "tflops": round(f / t_i / 1e12, 4),
+                    "matmul_only_ms": round(t_ii * 1e3, 3), "matmul_only_runs": n_ii,
+                    "matmul_only_gbs": round(b / t_ii / 1e9, 3), "matmul_only_tflops": round(f / t_ii / 1e12, 4)}
+        log(f"cpu {h8.name} M={m}: {t_i * 1e3:.1f} ms/call, matmul only {t_ii * 1e3:.1f} ms")
+    w1 = whole[1]
+    res.update({"value": w1["gbs"], "ms_per_call": w1["ms_per_call"], "matmul_only_gbs": w1["matmul_only_gbs"],
+                "prefill": whole[2048]})
+    res["sample"] = (f"{w1['runs']} whole calls of the torch CPU dequant-then-matmul path at {h8.name} M=1 "
+                     f"(median {w1['ms_per_call']:.1f} ms/call) and {whole[2048]['runs']} at M=2048 "
+                     f"(median {whole[2048]['ms_per_call']:.1f} ms/call), each after one warm-up; "
+                     "matmul-only variants on pre-dequantized bf16 weights beside them")
+    if quick:
+        return res
+    pts = []
+    rest = max(4.0, budget_s - (time.perf_counter() - t_start))
+    plan = (("qwen3-1.7b", (1, 4, 8), "cpu", None), ("qwen3-8b", (16, 64, 256, 512), "cpu", None),
+            ("qwen3-32b", (1, 512), "cuda", 4))
+    for name, ms_, gen, frac in plan:
+        shp = SHAPES[name]
+        mats = mats8 if name == h8.name else mats_for(shp, gen)
+        if frac is None:
+            t_dq, n_dq = _timed(lambda: dequant_all(mats), 3, rest / 10)
+        else:   # a quarter of each matrix's rows, scaled by 4 (elementwise work)
+            part = [a[: a.shape[0] // frac] for a in mats]
+            t_dq, n_dq = _timed(lambda: dequant_all(part), 3, rest / 10)
+            t_dq *= frac
+        wts = dequant_all(mats)
+        scale = shp.layers
+        for m in ms_:
+            x = activations(m, shp.hidden, device="cpu")
+            t_mm, n_mm = _timed(lambda: om.mlp_reference(x, *mats, weights=wts), 5, rest / 20)
+            t_i = (t_dq + t_mm) * scale
+            b = shp.layers * alg_bytes(m, shp.hidden, shp.inter)
+            f = shp.layers * alg_flops(m, shp.hidden, shp.inter)
+            note = "dequant and matmul timed separately, summed"
+            if shp.layers > 1:
+                note += (f"; one layer timed (dequant on 1/{frac} of its rows x{frac}), x{shp.layers} layers "
+                         "(extrapolated)")
+            pts.append({"config": name + (f" x{shp.layers} layers" if shp.layers > 1 else ""), "m": m,
+                        "ms_per_call": round(t_i * 1e3, 3), "gbs": round(b / t_i / 1e9, 3),
+                        "tflops": round(f / t_i / 1e12, 4), "matmul_only_ms": round(t_mm * scale * 1e3, 3),
+                        "matmul_only_gbs": round(b / (t_mm * scale) / 1e9, 3),
+                        "dequant_ms": round(t_dq * scale * 1e3, 3), "runs": [n_dq, n_mm], "note": note})
+            log(f"cpu {name} M={m}: {t_i * 1e3:.1f} ms/call (dequant {t_dq * scale * 1e3:.1f})")
+        del mats, wts
+    res["points"] = pts
+    return res
+
+
+# ----------------------------------------------------------------- profiles
+
+def committed_profile(name):
+    """A JSON summary committed under profiles/ (rocprofv3 counters of a
+    kernel on a workload, with the commands that produced it); None if absent."""
+    try:
+        with open(os.path.join(PROFILE_DIR, name)) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
+
 
 def committed_traffic(kernel, workload):
     """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE +
     WRITE_SIZE, scaled by the copy-kernel calibration), committed under
     profiles/ as traffic_<kernel>_<workload>.json; None if absent."""
-    path = os.path.join(PROFILE_DIR, f"traffic_{kernel}_{workload}.json")
-    try:
-        with open(path) as f:
-            return json.load(f).get("bytes_per_launch")
-    except (OSError, ValueError):
-        return None
+    rec = committed_profile(f"traffic_{kernel}_{workload}.json")
+    return rec.get("bytes_per_launch") if rec else None
 
 
-# ----------------------------------------------------------------- main
+# ----------------------------------------------------------------- GPU points
 
-def measure_point(capi, shape, m, sets, steps, path=0, reps=3):
-    import torch
+def measure_point(capi, shape, m, sets, steps, path=0):
     from tinyinfer_amd.workloads import activations, alg_bytes, alg_flops
     x = activations(m, shape.hidden, device="cuda")
     r = Runner(capi, x, sets, "mlp", path)
-    per = r.time_graph(steps, reps=reps)
-    ms = statistics.median(per)
+    r.warm(5)
+    per, _ = r.time_graph(steps)
+    p10, ms, p90 = quantiles(per)
     b, f = alg_bytes(m, shape.hidden, shape.inter), alg_flops(m, shape.hidden, shape.inter)
     return {"config": shape.name, "m": m, "us_per_call": round(ms * 1e3, 3),
+            "us_p10_p90": [round(p10 * 1e3, 3), round(p90 * 1e3, 3)],
             "gbs": round(b / ms / 1e6, 1), "tflops": round(f / ms / 1e9, 2),
             "hbm_frac": round(b / ms / 1e6 / HBM_PEAK_GBS, 4),
             "mfma_frac": round(f / ms / 1e9 / BF16_PEAK_TFLOPS, 4),
-            "tok_s": round(m / (ms * 1e-3), 1), "steps": steps, "weight_sets": len(sets)}
+            "tok_s": round(m / (ms * 1e-3), 1), "timed_calls": steps * len(per), "weight_sets": len(sets)}
 
 
-def measure_stack(capi, m, reps=5):
+def measure_stack(capi, m, layers, reps=5):
     """BASELINE's Qwen3-32B config: 64 MLP layers (hidden 5120, intermediate
     25600, ~13.4 GB of MXFP4 weights, far beyond the MALL) with the residual
-    add between layers; one graph per pass (x reset from x0 inside it)."""
+    add between layers; one graph per pass (x reset from x0 inside it).  On
+    these synthetic weights the plain stack overflows bf16 after a few layers
+    (the MLP is quadratic in x); the speed of the kernels does not depend on
+    the activation values."""
     import torch
-    from tinyinfer_amd.workloads import SHAPES, activations, alg_bytes, alg_flops, mlp_stack_step, quantized_weights
+    from tinyinfer_amd.workloads import SHAPES, activations, alg_bytes, alg_flops, mlp_stack_step
     shp = SHAPES["qwen3-32b"]
-    layers = [quantized_weights(shp.hidden, shp.inter, layer=l, generator="cuda") for l in range(shp.layers)]
     x0 = activations(m, shp.hidden, device="cuda")
     x = x0.clone()
     out = torch.empty_like(x0)
@@ -286,16 +377,49 @@ def measure_stack(capi, m, reps=5):
         b.record()
         torch.cuda.synchronize()
         per.append(a.elapsed_time(b))
-    del g, layers
-    torch.cuda.empty_cache()
-    ms = statistics.median(per)
+    del g
+    p10, ms, p90 = quantiles(per)
     byt = shp.layers * alg_bytes(m, shp.hidden, shp.inter)
     fl = shp.layers * alg_flops(m, shp.hidden, shp.inter)
     return {"config": f"{shp.name} x{shp.layers} layers + residual", "m": m, "ms_per_pass": round(ms, 4),
+            "ms_p10_p90": [round(p10, 4), round(p90, 4)],
             "tok_s": round(m / (ms * 1e-3), 1), "gbs": round(byt / ms / 1e6, 1),
             "hbm_frac": round(byt / ms / 1e6 / HBM_PEAK_GBS, 4), "tflops": round(fl / ms / 1e9, 2),
-            "mfma_frac": round(fl / ms / 1e9 / BF16_PEAK_TFLOPS, 4), "reps": reps,
-            "note": "residual add fused into each layer's down epilogue (in place), included in the time"}
+            "mfma_frac": round(fl / ms / 1e9 / BF16_PEAK_TFLOPS, 4), "timed_calls": reps * shp.layers,
+            "note": "residual add fused into each layer's down epilogue (in place), included in the time; "
+                    "weights drawn with the GPU generator (64 x 3 seeded N(0,0.02) matrices)"}
+
+
+def stage_roofline(capi, x, sets, steps, m, shape, bound):
+    """The gate_up stage (the MLP's dominant kernel) timed alone; down beside it."""
+    h, i = shape.hidden, shape.inter
+    gu = Runner(capi, x, sets, "gate_up")
+    gu.warm(3)
+    gu_ms = statistics.median(gu.time_graph(steps)[0])
+    dn = Runner(capi, x, sets, "down")
+    dn.warm(3)
+    dn_ms = statistics.median(dn.time_graph(steps)[0])
+    workload = f"{shape.name}-m{m}"
+    if bound == "hbm":
+        gu_bytes = 2 * i * h // 2 + 2 * i * h // 32 + 2 * m * h + 2 * m * i
+        ach = gu_bytes / (gu_ms * 1e-3) / 1e9
+        return {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": committed_traffic("gate_up", workload),
+                "kernel": ("gate_up stage: rowstream_kernel (1 KB single-row loads, MFMA diagonal dot "
+                           "products, SiLU*up epilogue)" if m == 1 else "gate_up stage"),
+                "us_per_launch": round(gu_ms * 1e3, 3), "alg_bytes_per_launch": gu_bytes,
+                "down_us_per_launch": round(dn_ms * 1e3, 3)}
+    gu_flops = 4 * m * h * i
+    ach = gu_flops / (gu_ms * 1e-3) / 1e12
+    busy = committed_profile(f"mfma_gate_up_gemm_{workload}.json")
+    return {"bound": "mfma", "achieved": round(ach, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(ach / BF16_PEAK_TFLOPS, 4), "traffic": committed_traffic("gate_up_gemm", workload),
+            "kernel": "gate_up stage: gemm_ring_kernel (direct-to-LDS ring, dequant to bf16, "
+                      "v_mfma_f32_32x32x16_bf16, SiLU*up epilogue)",
+            "us_per_launch": round(gu_ms * 1e3, 3), "alg_flops_per_launch": gu_flops,
+            "down_us_per_launch": round(dn_ms * 1e3, 3),
+            "down_tflops": round(2 * m * h * i / (dn_ms * 1e-3) / 1e12, 1),
+            "mfma_busy": busy.get("mfma_busy") if busy else None}
 
 
 def main():
@@ -311,7 +435,7 @@ def main():
         sys.exit(1)
     from tinyinfer_amd import capi
     from tinyinfer_amd.extension import load_extension
-    from tinyinfer_amd.workloads import SHAPES, activations, alg_bytes, alg_flops
+    from tinyinfer_amd.workloads import SHAPES, activations, alg_bytes, quantized_weights
 
     capi.lib()
     load_extension()
@@ -338,63 +462,33 @@ def main():
 
     if args.only:
         kind = {"decode": "mlp", "gate_up": "gate_up", "down": "down", "prefill": "mlp",
-                "norm_mlp": "norm_mlp"}[args.only]
-        mm = args.prefill_m if args.only == "prefill" else m
+                "prefill_gate_up": "gate_up", "prefill_down": "down", "norm_mlp": "norm_mlp"}[args.only]
+        mm = args.prefill_m if args.only.startswith("prefill") else m
         r = Runner(capi, activations(mm, shape.hidden, device="cuda"), sets, kind, path=args.path)
-        for s in range(args.warmup):
-            r.step(s)
-        torch.cuda.synchronize()
-        per = r.time_graph(args.steps, reps=1)
+        r.warm(args.warmup)
+        per, _ = r.time_graph(args.steps, reps=1)
         print(json.dumps({"only": args.only, "m": mm, "us_per_call": round(per[0] * 1e3, 3)}))
         return
 
-    # -- headline: K steps of the M=m MLP, one graph, one replay -------------
+    # -- headline: R replays of a K-step graph of the M=m MLP -----------------
     runner = Runner(capi, x, sets, "mlp")
-    for s in range(args.warmup):
-        runner.step(s)
-    torch.cuda.synchronize()
-    g = runner.graph(args.steps)
-    torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    ev0.record()
-    g.replay()
-    ev1.record()
-    torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3
-    ms_total = ev0.elapsed_time(ev1)
-    ms_step = ms_total / args.steps
-    del g
+    runner.warm(args.warmup)
+    per, wall = runner.time_graph(args.steps)
+    p10, ms_step, p90 = quantiles(per)
     b1 = alg_bytes(m, shape.hidden, shape.inter)
     value = b1 / (ms_step * 1e-3) / 1e9
-    log(f"M={m}: {ms_step * 1e3:.2f} us/step, {value:.1f} GB/s")
-    # distribution over further replays (10 replays of a K/10-step graph)
-    dist = runner.time_graph(max(1, args.steps // 10), reps=10)
+    log(f"M={m}: {ms_step * 1e3:.2f} us/step (median of {len(per)} replays x {args.steps} steps), "
+        f"{value:.1f} GB/s")
     py_us = eager_call_us(runner)
-
-    # -- dominant kernel: the gate_up stage alone ------------------------------
-    gu = Runner(capi, x, sets, "gate_up")
-    gu_ms = statistics.median(gu.time_graph(args.steps, reps=3))
-    h, i = shape.hidden, shape.inter
-    gu_bytes = 2 * i * h // 2 + 2 * i * h // 32 + 2 * m * h + 2 * m * i
-    gu_gbs = gu_bytes / (gu_ms * 1e-3) / 1e9
-    dn = Runner(capi, x, sets, "down")
-    dn_ms = statistics.median(dn.time_graph(args.steps, reps=3))
-    workload = f"{shape.name}-m{m}"
-    roofline = {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": committed_traffic("gate_up", workload),
-                "kernel": ("gate_up stage: rowstream_kernel (1 KB single-row loads, MFMA diagonal dot "
-                           "products, SiLU*up epilogue)" if m == 1 else
-                           "gate_up stage: stream_kernel (row-group dequant GEMV on MFMA, SiLU*up epilogue)"
-                           if m <= 8 else "gate_up stage: skinny dequant MFMA kernel"),
-                "us_per_launch": round(gu_ms * 1e3, 3), "alg_bytes_per_launch": gu_bytes,
-                "down_us_per_launch": round(dn_ms * 1e3, 3)}
+    roofline = stage_roofline(capi, x, sets, args.steps, m, shape, "hbm")
 
     # -- the decoder layer's MLP half: RMSNorm + MLP + residual ----------------
-    # fused (norm in gate_up's prologue, residual in down's epilogue) against
-    # the norm as a kernel of its own in front of the MLP-with-residual
-    nm_ms = statistics.median(Runner(capi, x, sets, "norm_mlp").time_graph(args.steps, reps=3))
-    sep_ms = statistics.median(Runner(capi, x, sets, "norm_then_mlp").time_graph(args.steps, reps=3))
+    nm = Runner(capi, x, sets, "norm_mlp")
+    nm.warm(3)
+    nm_ms = statistics.median(nm.time_graph(args.steps)[0])
+    sp = Runner(capi, x, sets, "norm_then_mlp")
+    sp.warm(3)
+    sep_ms = statistics.median(sp.time_graph(args.steps)[0])
     decoder_half = {"what": "x + MLP(RMSNorm(x)) per call, M=%d" % m,
                     "fused_us": round(nm_ms * 1e3, 3), "norm_kernel_then_mlp_us": round(sep_ms * 1e3, 3)}
     log(f"decoder half: fused {nm_ms * 1e3:.2f} us, norm kernel + MLP {sep_ms * 1e3:.2f} us")
@@ -402,41 +496,59 @@ def main():
     # -- prefill headline -------------------------------------------------------
     prefill = None
     if args.prefill_m:
-        pt = measure_point(capi, shape, args.prefill_m, sets, args.prefill_steps)
+        psteps = min(args.steps, 20)
+        pt = measure_point(capi, shape, args.prefill_m, sets, psteps)
+        xp = activations(args.prefill_m, shape.hidden, device="cuda")
         prefill = {"m": args.prefill_m, "tflops": pt["tflops"], "frac": pt["mfma_frac"],
-                   "us_per_call": pt["us_per_call"], "gbs": pt["gbs"], "tok_s": pt["tok_s"]}
+                   "us_per_call": pt["us_per_call"], "us_p10_p90": pt["us_p10_p90"], "gbs": pt["gbs"],
+                   "tok_s": pt["tok_s"], "timed_calls": pt["timed_calls"],
+                   "roofline": stage_roofline(capi, xp, sets, psteps, args.prefill_m, shape, "mfma")}
+        del xp
         log(f"M={args.prefill_m}: {pt['us_per_call']:.1f} us/call, {pt['tflops']:.1f} TFLOP/s")
 
     points = []
-    if args.all:
-        for name, ms_ in (("qwen3-1.7b", (1, 4, 8)), ("qwen3-8b", (16, 64, 256, 512))):
-            shp = SHAPES[name]
-            st = sets if name == shape.name else weight_sets(shp)
-            for mm in ms_:
-                points.append(measure_point(capi, shp, mm, st, 200 if mm <= 8 else 50))
-                log(json.dumps(points[-1]))
-            del st
-        torch.cuda.empty_cache()
-        for mm in (1, 512):
-            points.append(measure_stack(capi, mm))
+    if not args.quick:
+        for mm in (16, 64, 256, 512):
+            points.append(measure_point(capi, shape, mm, sets, 50 if mm <= 64 else 20))
             log(json.dumps(points[-1]))
+        del sets
+        torch.cuda.empty_cache()
+        shp = SHAPES["qwen3-1.7b"]
+        st = weight_sets(shp)
+        for mm in (1, 4, 8):
+            points.append(measure_point(capi, shp, mm, st, args.steps))
+            log(json.dumps(points[-1]))
+        del st
+        torch.cuda.empty_cache()
+        shp = SHAPES["qwen3-32b"]
+        t0 = time.perf_counter()
+        layers = [quantized_weights(shp.hidden, shp.inter, layer=l, generator="cuda") for l in range(shp.layers)]
+        torch.cuda.synchronize()
+        log(f"{shp.layers} layers of {shp.name} ready in {time.perf_counter() - t0:.1f}s")
+        for mm in (1, 512):
+            points.append(measure_stack(capi, mm, layers))
+            log(json.dumps(points[-1]))
+        del layers
+        torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu:
         log(f"timing the CPU baseline (~{args.cpu_seconds:.0f}s)")
-        cpu = cpu_baseline(shape, m, args.cpu_seconds)
+        cpu = cpu_baseline(args.cpu_seconds, args.quick)
 
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 6),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic: seeded N(0,0.02) weights quantized to MXFP4 on device, N(0,1) bf16 activations",
+        "data": "synthetic: seeded N(0,0.02) weights (torch CPU generator) quantized to MXFP4 on device, "
+                "N(0,1) bf16 activations",
         "config": {"workload": f"{shape.name} MXFP4 MLP (hidden {shape.hidden}, intermediate {shape.inter}) "
-                               f"decode M={m}, {len(sets)} rotated weight sets",
+                               f"decode M={m}, {len(runner.sets)} rotated weight sets",
                    "hidden": shape.hidden, "intermediate": shape.inter, "m": m},
         "hbm_frac": round(value / HBM_PEAK_GBS, 4),
-        "us_per_step_p10_p50_p90": [round(1e3 * q, 3) for q in _quantiles(dist)],
-        "wall_ms_timed_region": round(wall_ms, 3),
+        "timed_calls": args.steps * len(per), "replays": len(per),
+        "us_per_step_p10_p50_p90": [round(1e3 * q, 3) for q in (p10, ms_step, p90)],
+        "wall_ms_timed_region": round(wall * 1e3, 3),
         "python_call_us": round(py_us, 2),
         "roofline": roofline,
         "decoder_half": decoder_half,
@@ -446,12 +558,6 @@ def main():
         "device": dev_name,
     }
     print(json.dumps(line), flush=True)
-
-
-def _quantiles(v):
-    s = sorted(v)
-    pick = lambda q: s[min(len(s) - 1, int(round(q * (len(s) - 1))))]
-    return pick(0.1), pick(0.5), pick(0.9)
 
 
 if __name__ == "__main__":

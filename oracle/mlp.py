@@ -37,30 +37,35 @@ import numpy as np
 import torch
 import torch.nn.functional as F
 
-from .mxfp4 import dequantize_chunk
+from .mxfp4 import dequantize_chunk, dequantize_chunk_torch
 
 
 def _as_tensor(a) -> torch.Tensor:
     return a if isinstance(a, torch.Tensor) else torch.from_numpy(np.ascontiguousarray(a))
 
 
-def dequant_weight(packed, scale, dtype=torch.bfloat16) -> torch.Tensor:
-    """fp32 dequant then cast to the activation dtype (exact for bf16)."""
+def dequant_weight(packed, scale, dtype=torch.bfloat16, impl: str = "numpy") -> torch.Tensor:
+    """fp32 dequant then cast to the activation dtype (exact for bf16).
+    ``impl="torch"`` decodes with torch CPU ops (the reference's own form,
+    multi-threaded; same bits)."""
+    if impl == "torch":
+        return dequantize_chunk_torch(_as_tensor(packed).cpu(), _as_tensor(scale).cpu()).to(dtype)
     w32 = dequantize_chunk(_as_tensor(packed).cpu().numpy(), _as_tensor(scale).cpu().numpy())
     return torch.from_numpy(w32).to(dtype)
 
 
-def mlp_reference(x, gp, gs, up, us, dp, ds, weights=None) -> torch.Tensor:
+def mlp_reference(x, gp, gs, up, us, dp, ds, weights=None, impl: str = "numpy") -> torch.Tensor:
     """Reference torch CPU path; returns a CPU tensor of ``x``'s dtype.
 
     ``weights`` may carry pre-dequantized ``(Wg, Wu, Wd)`` in the activation
-    dtype to time the matmul-only variant."""
+    dtype to time the matmul-only variant; ``impl`` picks the decode form of
+    ``dequant_weight``."""
     xt = _as_tensor(x).cpu()
     dt = xt.dtype
     if weights is None:
-        wg = dequant_weight(gp, gs, dt)
-        wu = dequant_weight(up, us, dt)
-        wd = dequant_weight(dp, ds, dt)
+        wg = dequant_weight(gp, gs, dt, impl)
+        wu = dequant_weight(up, us, dt, impl)
+        wd = dequant_weight(dp, ds, dt, impl)
     else:
         wg, wu, wd = weights
     g = F.linear(xt, wg)

@@ -88,6 +88,30 @@ def dequantize_chunk(packed, scale, nan_ok: bool = False) -> np.ndarray:
         return (vals * mult).astype(np.float32).reshape(rows, k)
 
 
+def dequantize_chunk_torch(packed, scale) -> torch.Tensor:
+    """The same decode as torch CPU ops on torch tensors, the way the
+    reference's CPU path runs it (quantize_mxfp4.py:67-85: nibbles split,
+    table lookup, sign select, ``ldexp`` of the block exponent, one multiply
+    per block): this is the form the CPU baseline times, since torch spreads
+    it over the host's threads.  Raises on byte 255 like the reference.
+    Bit-identical to ``dequantize_chunk`` (tests/test_oracle_codec.py)."""
+    p = torch.as_tensor(np.asarray(packed, dtype=np.uint8)) if not isinstance(packed, torch.Tensor) else packed
+    s = torch.as_tensor(np.asarray(scale, dtype=np.uint8)) if not isinstance(scale, torch.Tensor) else scale
+    if p.ndim != 2 or s.ndim != 2 or p.shape[0] != s.shape[0]:
+        raise ValueError("packed/scale shape mismatch")
+    rows, half_k = p.shape
+    k = 2 * half_k
+    if k % BLOCK or s.shape[1] != k // BLOCK:
+        raise ValueError("scale shape mismatch")
+    if bool((s == E8M0_NAN).any()):
+        raise ValueError("E8M0 NaN scale detected (255)")
+    codes = torch.stack((p & 0x0F, p >> 4), dim=-1).reshape(rows, k)
+    mag = torch.from_numpy(E2M1_MAGNITUDE)[(codes & 7).long()]
+    vals = torch.where(codes >= 8, -mag, mag)
+    mult = torch.ldexp(torch.ones(s.shape, dtype=torch.float32), s.to(torch.int32) - E8M0_BIAS)
+    return (vals.reshape(rows, k // BLOCK, BLOCK) * mult.unsqueeze(-1)).reshape(rows, k)
+
+
 def block_exponent(amax: np.ndarray) -> np.ndarray:
     """Shared exponent per block: ``ceil(log2(amax / 6))`` evaluated with
     torch's fp32 CPU ops, 0 for all-zero blocks (quantize_mxfp4.py:42-46)."""

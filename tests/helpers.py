@@ -38,11 +38,13 @@ def assert_parity(out, ref, what=""):
     return st
 
 
-def torch_fp32_reference(x, gp, gs, up, us, dp, ds):
+def torch_fp32_reference(x, gp, gs, up, us, dp, ds, acc=torch.float32):
     """GPU fp32 reference of the dequant-then-matmul path, built from plain
     torch ops (table lookup + ldexp, as the reference dequantize_chunk does),
     sharing no code with the HIP kernels. h is rounded to x.dtype as in the
-    reference (its tmp buffer has the activation dtype)."""
+    reference (its tmp buffer has the activation dtype).  ``acc=float64``
+    gives the same composition with float64 sums (a second reference that
+    differs from the first only in its summation error)."""
     lut = torch.tensor([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0], device=x.device)
 
     def deq(p, s):
@@ -50,10 +52,10 @@ def torch_fp32_reference(x, gp, gs, up, us, dp, ds):
         v = lut[(codes & 7).long()]
         v = torch.where((codes & 8) != 0, -v, v)
         sc = torch.ldexp(torch.ones_like(s, dtype=torch.float32), s.to(torch.int32) - 127)
-        return (v.reshape(p.shape[0], -1, 32) * sc.unsqueeze(-1)).reshape(p.shape[0], -1)
+        return (v.reshape(p.shape[0], -1, 32) * sc.unsqueeze(-1)).reshape(p.shape[0], -1).to(acc)
 
-    xf = x.float()
+    xf = x.to(acc)
     g = xf @ deq(gp, gs).T
     u = xf @ deq(up, us).T
-    h = (torch.nn.functional.silu(g) * u).to(x.dtype).float()
+    h = (torch.nn.functional.silu(g) * u).to(x.dtype).to(acc)
     return (h @ deq(dp, ds).T).to(x.dtype)

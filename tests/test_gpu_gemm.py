@@ -106,7 +106,7 @@ def test_gemm_deterministic_and_full_call(capi):
     check_close(a.cpu(), om.mlp_kernel_semantics(x, *mats), "1.7B m=300 full")
 
 
-@pytest.mark.parametrize("m", [96, 128, 384])
+@pytest.mark.parametrize("m", [96, 128, 384, 512])
 def test_gemm_split_k_qwen3_8b(capi, m):
     """Qwen3-8B shapes at token counts whose tiles leave CUs idle: down has 16
     output tiles per 128 tokens, so its K (12288) is split."""

@@ -135,7 +135,7 @@ def test_golden_fixture(capi):
         assert_parity(out, ref, f"golden path={path}")
 
 
-@pytest.mark.parametrize("m", [1, 256, 2048])
+@pytest.mark.parametrize("m", [1, 256, 512, 2048])
 def test_qwen3_8b_against_torch_fp32_reference(capi, m):
     """Full 8B shape (gate/up [12288,4096], down [4096,12288]); reference is a
     torch fp32 GPU dequant-then-matmul built from plain torch ops."""

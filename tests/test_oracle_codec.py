@@ -79,6 +79,25 @@ def test_dequant_values_are_exact_in_bf16():
     assert np.isinf(f[254, 15]) and f[254, 15] < 0
 
 
+def test_torch_form_of_dequant_is_bit_identical():
+    """The torch-ops decode the CPU baseline times gives the numpy decode's
+    bits on the exhaustive code x byte table and on random blocks, and
+    raises on byte 255 and bad shapes like it."""
+    packed, scale = exhaustive_pairs()
+    a = ox.dequantize_chunk(packed, scale)
+    b = ox.dequantize_chunk_torch(packed, scale).numpy()
+    assert b.dtype == np.float32 and np.array_equal(f32_bits(a), f32_bits(b))
+    rng = np.random.default_rng(5)
+    p = rng.integers(0, 256, (37, 96), dtype=np.uint8)
+    s = rng.integers(0, 255, (37, 6), dtype=np.uint8)
+    assert np.array_equal(f32_bits(ox.dequantize_chunk(p, s)),
+                          f32_bits(ox.dequantize_chunk_torch(torch.from_numpy(p), torch.from_numpy(s)).numpy()))
+    with pytest.raises(ValueError):
+        ox.dequantize_chunk_torch(np.zeros((1, 16), np.uint8), np.array([[255]], np.uint8))
+    with pytest.raises(ValueError):
+        ox.dequantize_chunk_torch(np.zeros((1, 16), np.uint8), np.zeros((1, 2), np.uint8))
+
+
 def test_hand_built_bytes():
     # 0x21: low nibble 1 (0.5) first, high nibble 2 (1.0) second
     p = np.full((1, 16), 0x21, np.uint8)

@@ -38,6 +38,7 @@ SHAPES = {
 
 WEIGHT_STD = 0.02
 X_SEED = 7
+NORM_EPS = 1e-6          # Qwen3's rms_norm_eps
 
 
 def weight_bytes(h: int, i: int) -> int:
@@ -99,4 +100,23 @@ def mlp_stack_step(capi, x, layers, out, tmp, fused_residual=True):
         else:
             capi.mlp_forward(x, *w, out=out, tmp=tmp)
             x.add_(out)
+    return x
+
+
+def norm_weight(h: int, layer: int = 0, dtype=torch.bfloat16, device="cuda") -> torch.Tensor:
+    """A post-attention RMSNorm weight for ``layer``: 1 + N(0, 0.1), seed 2000 + layer."""
+    return (1.0 + 0.1 * _randn((h,), 2000 + layer, "cpu", None)).to(dtype).to(device)
+
+
+def decoder_stack_step(capi, x, layers, norm_ws, tmp, xn, eps: float = NORM_EPS):
+    """One pass over the decoder layers' MLP halves, in place on ``x``:
+    ``x <- x + MLP_l(RMSNorm_l(x))`` for every layer (the reference decoder
+    layer's ``post_attention_layernorm -> mlp -> residual add``,
+    tinyinfer/models/qwen3.py:210-219), each layer one call of the fused
+    entry point.  The norm keeps every MLP's input at unit RMS, so the
+    residual stream grows only as a random walk over the 64 layers; the plain
+    stack of ``mlp_stack_step`` squares its scale every layer and overflows
+    bf16 within a few layers on N(0, 0.02) weights."""
+    for w, nw in zip(layers, norm_ws):
+        capi.mlp_forward_rmsnorm(x, nw, eps, *w, out=x, tmp=tmp, xn=xn)
     return x
