@@ -8,6 +8,14 @@
  * it does. Every function returns 0 on success or a TI_* status code, and
  * never throws.
  *
+ * Threads: every function may be called from any host thread, also
+ * concurrently; calls on one stream are ordered by the stream.  The library's
+ * shared state (device properties, tuning options, split-K workspaces) is
+ * initialised once and guarded.  Split-K workspaces are per (device, stream):
+ * graphs captured on one stream share that stream's workspace, so replays of
+ * such graphs must not run at the same time as each other, or as calls on
+ * the capture stream.
+ *
  * Layout (reference tinyinfer/layers/linear.py:36-48,
  * tinyinfer/quantization/quantize_mxfp4.py:233-253):
  *   X           [N, hidden]                    bf16 or fp16, row-major
@@ -203,11 +211,51 @@ int tinyinfer_mxfp4_quantize(const void* w, int in_dtype, size_t rows, size_t k,
 /*
  * Diagnostics of the current device (synchronous): the number of times the
  * fused decode kernel's wait for the other workgroups gave up since the
- * library was loaded (a safety bound that only trips if its workgroups were
- * not all resident; results of such a call are invalid). No reference
- * counterpart.
+ * library was loaded or tinyinfer_mxfp4_decode_reset last ran (a safety bound
+ * that only trips if its workgroups were not all resident).  The result of
+ * the call that timed out is invalid, and while the count is nonzero every
+ * later TI_PATH_DECODE call returns TI_OK but leaves tmp and O unwritten (its
+ * kernel exits at entry). No reference counterpart.
  */
 int tinyinfer_mxfp4_diagnostics(uint32_t* decode_barrier_timeouts);
+
+/*
+ * Synchronizes the current device and clears the fused decode kernel's
+ * cross-workgroup state (flags, epoch, the poison left by a timed-out wait,
+ * the timeout count). No reference counterpart.
+ */
+int tinyinfer_mxfp4_decode_reset(void);
+
+/*
+ * Tuning options, by the name of the environment variable that sets each at
+ * load (TINYINFER_ROWSTREAM, TINYINFER_ROWPAIR, TINYINFER_TILE,
+ * TINYINFER_TILE_GU, TINYINFER_ROW_SPLIT_GATEUP, TINYINFER_ROW_SPLIT_DOWN,
+ * TINYINFER_GEMM_RING, TINYINFER_RING_KSPLIT, TINYINFER_RING_WR_GU / _DN,
+ * TINYINFER_RING_NW_GU / _DN, TINYINFER_SKINNY_NW, TINYINFER_STREAM_SPU_GU /
+ * _DN, TINYINFER_STREAM_XREG, TINYINFER_WORKSPACE_MB, TINYINFER_DECODE_SPIN).
+ * The environment is read once, at the first call that needs an option; set
+ * changes a value for every later call (atomically; a call already inside
+ * the library may see either value).  TI_ERR_INVALID_ARG for an unknown name
+ * or a value outside the option's range. No reference counterpart (kernel
+ * choice and tuning for tests and benchmarks).
+ */
+int tinyinfer_mxfp4_set_option(const char* name, int value);
+int tinyinfer_mxfp4_get_option(const char* name, int* value);
+
+/*
+ * Split-K workspaces (fp32 partial sums of the tile and GEMM kernels): the
+ * bytes held over all devices and streams, and the limit of one buffer
+ * (TINYINFER_WORKSPACE_MB; a call that would need more runs a kernel
+ * without one, or with fewer K ranges). No reference counterpart.
+ */
+int tinyinfer_mxfp4_workspace_info(size_t* bytes_held, size_t* limit_bytes);
+
+/*
+ * Synchronizes every device that holds a workspace and frees them all.  No
+ * graph captured before the call may be replayed after it (captured kernels
+ * hold the workspace's address). No reference counterpart.
+ */
+int tinyinfer_mxfp4_release_workspaces(void);
 
 /* Human-readable text for a TI_* status code (static storage). */
 const char* tinyinfer_mxfp4_status_string(int status);

@@ -48,10 +48,44 @@ def test_python_constants_match_header(capi):
 
 
 def test_abi_version_and_status_strings(capi):
-    assert capi.lib().tinyinfer_mxfp4_abi_version() == 5
+    assert capi.lib().tinyinfer_mxfp4_abi_version() == 6
     assert capi.status_string(0) == "ok"
     assert "32" in capi.status_string(capi.TI_ERR_BAD_SHAPE)
     assert capi.status_string(999) == "unknown status"
+
+
+def test_tuning_options(capi):
+    """Options start from the environment (read once) and change through the
+    C ABI; unknown names and out-of-range values are refused; the context
+    manager restores the previous value."""
+    assert capi.get_option("TINYINFER_TILE") in (0, 1)
+    before = capi.get_option("TINYINFER_RING_KSPLIT")
+    with capi.option("TINYINFER_RING_KSPLIT", 5):
+        assert capi.get_option("TINYINFER_RING_KSPLIT") == 5
+    assert capi.get_option("TINYINFER_RING_KSPLIT") == before
+    for name, bad in (("TINYINFER_ROW_SPLIT_DOWN", 3), ("TINYINFER_RING_NW_GU", 6), ("TINYINFER_TILE", 2),
+                      ("TINYINFER_RING_KSPLIT", -1), ("TINYINFER_NO_SUCH_OPTION", 1)):
+        with pytest.raises(capi.TinyInferError) as e:
+            capi.set_option(name, bad)
+        assert e.value.status == capi.TI_ERR_INVALID_ARG
+    assert capi.lib().tinyinfer_mxfp4_set_option(None, 1) == capi.TI_ERR_INVALID_ARG
+    held, limit = capi.workspace_info()
+    assert held >= 0 and limit == capi.get_option("TINYINFER_WORKSPACE_MB") << 20
+
+
+def test_options_from_environment_read_once():
+    """A fresh process takes the options from its environment."""
+    import subprocess
+    import sys
+    code = ("from tinyinfer_amd import capi; "
+            "print(capi.get_option('TINYINFER_TILE'), capi.get_option('TINYINFER_ROW_SPLIT_DOWN'), "
+            "capi.get_option('TINYINFER_RING_NW_GU'))")
+    env = dict(os.environ, TINYINFER_TILE="0", TINYINFER_ROW_SPLIT_DOWN="2", TINYINFER_RING_NW_GU="5")
+    out = subprocess.run([sys.executable, "-c", code], cwd=ROOT, env=env, capture_output=True, text=True,
+                         timeout=120)
+    assert out.returncode == 0, out.stderr
+    # an invalid value (5 waves) leaves the default
+    assert out.stdout.split() == ["0", "2", "8"]
 
 
 def test_validation_before_device_work(capi):

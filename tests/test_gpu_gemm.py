@@ -116,25 +116,25 @@ def test_gemm_split_k_qwen3_8b(capi, m):
 
 
 @pytest.mark.parametrize("ksplit", [1, 2, 3, 5])
-def test_gemm_forced_split_counts(capi, ksplit, monkeypatch):
+def test_gemm_forced_split_counts(capi, ksplit):
     """Every split count gives the oracle's result within tolerance, also
     uneven ranges (5 ranges over 6 blocks of 512 K) and no split at all."""
-    monkeypatch.setenv("TINYINFER_RING_KSPLIT", str(ksplit))
     banner(f"gemm forced ksplit={ksplit}")
     x, mats = make_case(200, 3072, 3072, seed=600 + ksplit)
-    run_gemm_stages(capi, x, mats, f"ksplit={ksplit}")
+    with capi.option("TINYINFER_RING_KSPLIT", ksplit):
+        run_gemm_stages(capi, x, mats, f"ksplit={ksplit}")
 
 
-def test_gemm_split_deterministic(capi, monkeypatch):
+def test_gemm_split_deterministic(capi):
     """Split results are bit-reproducible and close to the unsplit ones."""
     banner("gemm split determinism")
     x, mats = make_case(160, 2048, 6144, seed=31)
     xd, md = to_dev(x, mats)
-    monkeypatch.setenv("TINYINFER_RING_KSPLIT", "4")
-    a = capi.mlp_forward(xd, *md, path=GEMM)
-    b = capi.mlp_forward(xd, *md, path=GEMM)
-    monkeypatch.setenv("TINYINFER_RING_KSPLIT", "1")
-    c = capi.mlp_forward(xd, *md, path=GEMM)
+    with capi.option("TINYINFER_RING_KSPLIT", 4):
+        a = capi.mlp_forward(xd, *md, path=GEMM)
+        b = capi.mlp_forward(xd, *md, path=GEMM)
+    with capi.option("TINYINFER_RING_KSPLIT", 1):
+        c = capi.mlp_forward(xd, *md, path=GEMM)
     torch.cuda.synchronize()
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
     check_close(a.cpu(), c.cpu().float(), "split vs unsplit")

@@ -12,7 +12,6 @@ the residual and the RMSNorm prologue.  TINYINFER_ROWPAIR=0 switches the
 library back to the row / 8-row stream kernels, which the last tests compare
 against."""
 
-import os
 
 import numpy as np
 import pytest
@@ -121,11 +120,8 @@ def test_rowpair_matches_other_decode_kernels(capi, m, launches):
     xd, md = to_dev(x, mats)
     out, names = {}, {}
     for flag in ("1", "0"):
-        os.environ["TINYINFER_ROWPAIR"] = flag
-        try:
+        with capi.option("TINYINFER_ROWPAIR", int(flag)):
             names[flag] = kernel_names(lambda: out.__setitem__(flag, capi.mlp_forward(xd, *md, path=SKINNY)))
-        finally:
-            del os.environ["TINYINFER_ROWPAIR"]
     ref = om.mlp_kernel_semantics(x, *mats)
     check_close(out["1"].cpu(), ref, "row-pair kernels")
     check_close(out["0"].cpu(), ref, "other kernels")

@@ -11,7 +11,6 @@ range (NaN included), fp16 activations, the residual and the RMSNorm
 prologue.  TINYINFER_ROWSTREAM=0 switches the library back to the 8-row
 stream kernels for N == 1, which the last tests compare against."""
 
-import os
 
 import numpy as np
 import pytest
@@ -158,11 +157,8 @@ def test_rowstream_matches_item_stream_kernels(capi):
     out = {}
     names = {}
     for flag in ("1", "0"):
-        os.environ["TINYINFER_ROWSTREAM"] = flag
-        try:
+        with capi.option("TINYINFER_ROWSTREAM", int(flag)):
             names[flag] = kernel_names(lambda: out.__setitem__(flag, capi.mlp_forward(xd, *md, path=SKINNY)))
-        finally:
-            del os.environ["TINYINFER_ROWSTREAM"]
     ref = om.mlp_kernel_semantics(x, *mats)
     check_close(out["1"].cpu(), ref, "row kernels")
     check_close(out["0"].cpu(), ref, "item kernels")
@@ -181,14 +177,11 @@ def test_rowstream_down_split_override(capi, split):
     banner(f"rowstream down split {split}")
     x, mats = make_case(1, 4096, 12288, seed=321)
     xd, md = to_dev(x, mats)
-    os.environ["TINYINFER_ROW_SPLIT_DOWN"] = split
-    try:
+    with capi.option("TINYINFER_ROW_SPLIT_DOWN", int(split)):
         h = capi.gate_up(xd, *md[:4], path=SKINNY)
         out = capi.down(h, *md[4:], path=SKINNY)
         again = capi.down(h, *md[4:], path=SKINNY)
         torch.cuda.synchronize()
-    finally:
-        del os.environ["TINYINFER_ROW_SPLIT_DOWN"]
     assert torch.equal(out.view(torch.int16), again.view(torch.int16))
     check_close(out.cpu(), down_semantics(h.cpu(), mats[4], mats[5]), f"split {split}")
 
@@ -201,13 +194,10 @@ def test_rowstream_gateup_split_with_norm(capi):
     x, mats = make_case(1, 4096, 12288, seed=55)
     xd, md = to_dev(x, mats)
     w = (torch.rand(4096, generator=torch.Generator().manual_seed(4)) + 0.5).to(torch.bfloat16)
-    os.environ["TINYINFER_ROW_SPLIT_GATEUP"] = "2"
-    try:
+    with capi.option("TINYINFER_ROW_SPLIT_GATEUP", 2):
         out, xn = capi.mlp_forward_rmsnorm(xd, w.cuda(), 1e-6, *md, path=SKINNY)
         plain = capi.mlp_forward(xn, *md, path=SKINNY, residual=xd)
         torch.cuda.synchronize()
-    finally:
-        del os.environ["TINYINFER_ROW_SPLIT_GATEUP"]
     xn_ref = om.rmsnorm_reference(x, w, 1e-6)
     rel = ((xn.cpu().float() - xn_ref.float()).abs() / xn_ref.float().abs().clamp_min(1e-30)).max()
     assert float(rel) <= 2 ** -7, f"xn max rel {float(rel)}"
@@ -222,21 +212,26 @@ def test_rowstream_gateup_split_with_norm(capi):
     (1024, 25600),   # down over four waves (3, 3, 3, 4 chunks)
     (1024, 4096),    # down 2 chunks, one wave per row
 ])
-def test_rowstream_two_tokens(capi, h, i, monkeypatch):
+def test_rowstream_two_tokens(capi, h, i):
     """Two tokens (bf16) with the row-pair kernels off: the down stage runs on
     the row kernels, two MFMA passes over each dequantized operand, one per
     token's activations (gate_up on the 8-row stream kernel)."""
-    monkeypatch.setenv("TINYINFER_ROWPAIR", "0")
     banner(f"rowstream two tokens h={h} i={i}")
     x, mats = make_case(2, h, i, seed=5 * h + i)
-    stages(capi, x, mats, f"m=2 h={h} i={i}")
+    with capi.option("TINYINFER_ROWPAIR", 0):
+        stages(capi, x, mats, f"m=2 h={h} i={i}")
 
 
-def test_rowstream_two_tokens_norm_residual(capi, monkeypatch):
+@pytest.fixture
+def rowpair_off(capi):
+    with capi.option("TINYINFER_ROWPAIR", 0):
+        yield
+
+
+def test_rowstream_two_tokens_norm_residual(capi, rowpair_off):
     """x + MLP(RMSNorm(x)) at two tokens (row-pair kernels off): per-token
     norm sums in the prologue, per-token residual in the epilogue; equal to
     the unfused composition."""
-    monkeypatch.setenv("TINYINFER_ROWPAIR", "0")
     banner("rowstream two tokens norm + residual")
     x, mats = make_case(2, 4096, 12288, seed=77)
     xd, md = to_dev(x, mats)

@@ -31,11 +31,11 @@ def capi():
 
 
 @pytest.fixture(autouse=True)
-def stream_kernels_only(monkeypatch):
+def stream_kernels_only(capi):
     """The row and row-pair kernels take 1..4 tokens when they are on; these
     tests keep them off so that every case runs on the 8-row stream kernels."""
-    monkeypatch.setenv("TINYINFER_ROWSTREAM", "0")
-    monkeypatch.setenv("TINYINFER_ROWPAIR", "0")
+    with capi.option("TINYINFER_ROWSTREAM", 0), capi.option("TINYINFER_ROWPAIR", 0):
+        yield
 
 
 def h_semantics(x, gp, gs, up, us):

@@ -10,7 +10,6 @@ than waves, scale bytes outside the hardware conversion's exact range (NaN
 included), the residual, and the dispatch (TINYINFER_TILE=0 switches the
 kernels off)."""
 
-import os
 
 import numpy as np
 import pytest
@@ -103,11 +102,8 @@ def test_tile_dispatch_and_switch(capi):
     xd, md = to_dev(x, mats)
     out, names = {}, {}
     for flag in ("1", "0"):
-        os.environ["TINYINFER_TILE"] = flag
-        try:
+        with capi.option("TINYINFER_TILE", int(flag)):
             names[flag] = kernel_names(lambda: out.__setitem__(flag, capi.mlp_forward(xd, *md, path=AUTO)))
-        finally:
-            del os.environ["TINYINFER_TILE"]
     ref = om.mlp_kernel_semantics(x, *mats)
     check_close(out["1"].cpu(), ref, "tile kernels")
     check_close(out["0"].cpu(), ref, "GEMM path")
@@ -134,11 +130,8 @@ def test_tile_gate_up_in_one_launch(capi, m, h, i):
     xd, md = to_dev(x, mats)
     out, names = {}, {}
     for flag in ("1", "0"):
-        os.environ["TINYINFER_TILE_GU"] = flag
-        try:
+        with capi.option("TINYINFER_TILE_GU", int(flag)):
             names[flag] = kernel_names(lambda: out.__setitem__(flag, capi.gate_up(xd, *md[:4], path=SKINNY)))
-        finally:
-            del os.environ["TINYINFER_TILE_GU"]
     assert torch.equal(out["1"].view(torch.int16), out["0"].view(torch.int16))
     check_close(out["1"].cpu(), h_semantics(x, *mats[:4]), f"m={m} gate_up")
     if names["1"]:

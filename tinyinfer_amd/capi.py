@@ -52,6 +52,11 @@ SIGNATURES = {
     "tinyinfer_mxfp4_dequant": (_int, [_u8p, _u8p, _sz, _sz, _vp, _int, _vp]),
     "tinyinfer_mxfp4_quantize": (_int, [_vp, _int, _sz, _sz, _u8p, _u8p, _vp, _vp]),
     "tinyinfer_mxfp4_diagnostics": (_int, [ctypes.c_void_p]),
+    "tinyinfer_mxfp4_decode_reset": (_int, []),
+    "tinyinfer_mxfp4_set_option": (_int, [ctypes.c_char_p, _int]),
+    "tinyinfer_mxfp4_get_option": (_int, [ctypes.c_char_p, ctypes.c_void_p]),
+    "tinyinfer_mxfp4_workspace_info": (_int, [ctypes.c_void_p, ctypes.c_void_p]),
+    "tinyinfer_mxfp4_release_workspaces": (_int, []),
     "tinyinfer_mxfp4_status_string": (ctypes.c_char_p, [_int]),
     "tinyinfer_mxfp4_abi_version": (_int, []),
 }
@@ -219,6 +224,52 @@ def decode_barrier_timeouts() -> int:
     v = ctypes.c_uint32(0)
     _check(lib().tinyinfer_mxfp4_diagnostics(ctypes.byref(v)), "tinyinfer_mxfp4_diagnostics")
     return int(v.value)
+
+
+def decode_reset() -> None:
+    """Clear the fused decode kernel's cross-workgroup state (synchronous)."""
+    _check(lib().tinyinfer_mxfp4_decode_reset(), "tinyinfer_mxfp4_decode_reset")
+
+
+def set_option(name: str, value: int) -> None:
+    """Set a tuning option (see tinyinfer_mxfp4_set_option) for every later call."""
+    _check(lib().tinyinfer_mxfp4_set_option(name.encode(), int(value)), f"tinyinfer_mxfp4_set_option({name})")
+
+
+def get_option(name: str) -> int:
+    v = ctypes.c_int(0)
+    _check(lib().tinyinfer_mxfp4_get_option(name.encode(), ctypes.byref(v)), f"tinyinfer_mxfp4_get_option({name})")
+    return int(v.value)
+
+
+class option:
+    """Context manager: ``with option("TINYINFER_TILE", 0): ...`` sets a tuning
+    option for the block and restores the previous value after it."""
+
+    def __init__(self, name: str, value: int):
+        self.name, self.value = name, int(value)
+
+    def __enter__(self):
+        self.prev = get_option(self.name)
+        set_option(self.name, self.value)
+        return self
+
+    def __exit__(self, *exc):
+        set_option(self.name, self.prev)
+        return False
+
+
+def workspace_info():
+    """(bytes held by split-K workspaces over all devices/streams, limit per buffer)."""
+    held, limit = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    _check(lib().tinyinfer_mxfp4_workspace_info(ctypes.byref(held), ctypes.byref(limit)),
+           "tinyinfer_mxfp4_workspace_info")
+    return int(held.value), int(limit.value)
+
+
+def release_workspaces() -> None:
+    """Synchronize and free every split-K workspace (no earlier graph may be replayed afterwards)."""
+    _check(lib().tinyinfer_mxfp4_release_workspaces(), "tinyinfer_mxfp4_release_workspaces")
 
 
 def dequant(packed, scale, out_dtype=None, stream=None):

@@ -6,8 +6,6 @@
 // instead of thrown exceptions, so the boundary is safe for any FFI.
 #include <hip/hip_runtime.h>
 
-#include <atomic>
-#include <cstring>
 
 #include "../../include/tinyinfer_mxfp4.h"
 #include "mxfp4_common.hpp"
@@ -22,21 +20,9 @@ using tinyinfer::MlpArgs;
 constexpr size_t kMaxDim = size_t(1) << 30;
 constexpr size_t kMaxTokens = size_t(1) << 24;
 
-// Per-device "is gfx950" cache: 0 unknown, 1 yes, 2 no.
-std::atomic<int> g_arch_ok[64];
-
 int check_device() {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return TI_ERR_NO_DEVICE;
-  if (dev < 0 || dev >= 64) return TI_ERR_NO_DEVICE;
-  int st = g_arch_ok[dev].load(std::memory_order_relaxed);
-  if (st == 0) {
-    hipDeviceProp_t prop;
-    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return TI_ERR_NO_DEVICE;
-    st = (std::strncmp(prop.gcnArchName, "gfx950", 6) == 0) ? 1 : 2;
-    g_arch_ok[dev].store(st, std::memory_order_relaxed);
-  }
-  return st == 1 ? TI_OK : TI_ERR_NO_DEVICE;
+  const tinyinfer::DeviceInfo d = tinyinfer::device_info();
+  return d.cus > 0 && d.gfx950 ? TI_OK : TI_ERR_NO_DEVICE;
 }
 
 int to_status(hipError_t e) { return e == hipSuccess ? TI_OK : TI_ERR_HIP; }
@@ -300,6 +286,29 @@ int tinyinfer_mxfp4_diagnostics(uint32_t* decode_barrier_timeouts) {
   return TI_OK;
 }
 
-int tinyinfer_mxfp4_abi_version(void) { return 5; }
+int tinyinfer_mxfp4_decode_reset(void) {
+  const int st = check_device();
+  if (st != TI_OK) return st;
+  return to_status(tinyinfer::decode_reset());
+}
+
+int tinyinfer_mxfp4_set_option(const char* name, int value) {
+  return tinyinfer::set_option(name, value) ? TI_OK : TI_ERR_INVALID_ARG;
+}
+
+int tinyinfer_mxfp4_get_option(const char* name, int* value) {
+  return tinyinfer::get_option(name, value) ? TI_OK : TI_ERR_INVALID_ARG;
+}
+
+int tinyinfer_mxfp4_workspace_info(size_t* bytes_held, size_t* limit_bytes) {
+  if (!bytes_held || !limit_bytes) return TI_ERR_INVALID_ARG;
+  *bytes_held = tinyinfer::workspace_bytes_held();
+  *limit_bytes = tinyinfer::workspace_limit();
+  return TI_OK;
+}
+
+int tinyinfer_mxfp4_release_workspaces(void) { return to_status(tinyinfer::release_workspaces()); }
+
+int tinyinfer_mxfp4_abi_version(void) { return 6; }
 
 }  // extern "C"

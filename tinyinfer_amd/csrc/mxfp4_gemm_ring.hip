@@ -34,12 +34,8 @@
 // (a permutation of K shared by both operands leaves each dot product
 // unchanged).  A lane's W bytes for the step are then one 16-byte run under
 // one scale byte, and its X bytes one 64-byte run.
-#include <cstdlib>
-#include <map>
-#include <mutex>
 #include <type_traits>
 #include <utility>
-#include <vector>
 
 #include "mxfp4_common.hpp"
 #include "mxfp4_launch.hpp"
@@ -358,52 +354,21 @@ __global__ __launch_bounds__(256) void ring_reduce(const float* __restrict__ ws,
   *reinterpret_cast<u32x2_t*>(out + m * N + n) = with_residual4<kBF16>(u32x2_t{lo, hi}, res, m * N + n);
 }
 
-// Split-K workspace: one buffer per (device, stream), grown on demand.  A
-// buffer is never freed: a replaced one is kept for the life of the process,
-// because kernels still queued, and graphs captured with it, hold its
-// address.  Growth is refused during graph capture (allocation is not a
-// capturable operation); the call then runs unsplit.  So a graph gets the
-// split kernels when its capture stream has already run a call of at least
-// the same size eagerly (the usual warm-up).  Calls on one stream are
-// ordered, so they share its buffer; calls on other streams use their own.
-float* split_workspace(size_t bytes, hipStream_t st) {
-  static std::mutex mu;
-  static std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> bufs;
-  static std::vector<void*> retired;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
-  std::lock_guard<std::mutex> lock(mu);
-  auto& b = bufs[{dev, st}];
-  if (b.second >= bytes) return static_cast<float*>(b.first);
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
-    (void)hipGetLastError();
-    return nullptr;
-  }
-  const size_t want = (bytes + (64u << 20) - 1) & ~size_t((64u << 20) - 1);
-  void* p = nullptr;
-  if (hipMalloc(&p, want) != hipSuccess) {
-    (void)hipGetLastError();
-    return nullptr;
-  }
-  if (b.first) retired.push_back(b.first);
-  b = {p, want};
-  return static_cast<float*>(p);
-}
-
 // Number of K ranges per output tile.  Cost model (microseconds): a tile's
 // full-K time at ~5 TFLOP/s per CU, times the rounds of workgroups the split
 // grid needs on 256 CUs, divided by the split; plus the fp32 partials written
 // and read back (mostly from the 256 MB last-level cache) and the reduce
 // launch.  The smallest split with the least cost wins; K ranges are whole
-// 8-step blocks.  TINYINFER_RING_KSPLIT=<n> forces n (clamped), for tuning.
+// 8-step blocks, and the partials of all ranges fit the workspace limit.
+// The option TINYINFER_RING_KSPLIT=<n> forces n (clamped), for tuning.
 int ring_ksplit(const RingArgs& r, int bm, int nmat, int64_t tiles, int per_cu) {
   const int nblk = r.K / (8 * kBK);
   int cap = nblk < 32 ? nblk : 32;
-  if (const char* e = std::getenv("TINYINFER_RING_KSPLIT")) {
-    const int v = std::atoi(e);
-    if (v >= 1) return v < cap ? v : (cap > 0 ? cap : 1);
-  }
+  const size_t per_split = (size_t)r.M * nmat * r.N * sizeof(float);
+  const size_t fit = per_split ? workspace_limit() / per_split : 0;
+  if ((size_t)cap > fit) cap = (int)fit;
+  if (cap < 2) return 1;
+  if (const int v = option(kOptRingKsplit); v >= 1) return v < cap ? v : cap;
   // per_cu workgroups share a CU: each runs at 1 / per_cu of its rate
   const int64_t slots = 256 * per_cu;
   const double t_tile = 2.0 * bm * 256.0 * r.K / 5e6 * per_cu;
@@ -432,7 +397,7 @@ hipError_t launch_ring(RingArgs r, hipStream_t st) {
   const int ksplit_want = ring_ksplit(r, BM, NMAT, tiles, NW == 4 ? 2 : 1);
   int ksplit = 1;
   if (ksplit_want > 1) {
-    r.ws = split_workspace((size_t)ksplit_want * r.M * NMAT * r.N * sizeof(float), st);
+    r.ws = gemm_split_workspace((size_t)ksplit_want * r.M * NMAT * r.N * sizeof(float), st);
     if (r.ws) ksplit = ksplit_want;
   }
   r.ksplit = ksplit;
@@ -453,36 +418,17 @@ hipError_t launch_ring(RingArgs r, hipStream_t st) {
   return hipGetLastError();
 }
 
-// Wave layout override for tuning: TINYINFER_RING_WR_GU / _DN = 2 or 4.
-int ring_env_wr(const char* name) {
-  const char* e = std::getenv(name);
-  return (e && std::atoi(e) == 2) ? 2 : 4;
-}
-int ring_env_nw(const char* name) {
-  const char* e = std::getenv(name);
-  return (e && std::atoi(e) == 4) ? 4 : 8;
-}
-
 }  // namespace
 
 bool gemm_ring_supported(const MlpArgs& a, int stage) {
-  static const bool off = [] { const char* e = std::getenv("TINYINFER_GEMM_RING"); return e && e[0] == '0'; }();
-  if (off || a.dtype != kBF16) return false;
+  if (option(kOptGemmRing) == 0 || a.dtype != kBF16) return false;
   if ((stage & kStageGateUp) && a.hidden % 512 != 0) return false;
   if ((stage & kStageDown) && a.inter % 512 != 0) return false;
   if (a.n > (1 << 24) || a.hidden > (1 << 20) || a.inter > (1 << 22)) return false;
   const void* scales[] = {a.gate_scale, a.up_scale, a.down_scale};
   for (const void* p : scales)
     if (p && (reinterpret_cast<uintptr_t>(p) & 15u)) return false;
-  static int64_t lds_cache[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
-  if (lds_cache[dev] == 0) {
-    hipDeviceProp_t prop;
-    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return false;
-    lds_cache[dev] = (int64_t)prop.sharedMemPerBlock;
-  }
-  return lds_cache[dev] >= RingCfg<256, 8>::kLds;
+  return device_info().lds_per_block >= RingCfg<256, 8>::kLds;
 }
 
 // Token tiles of 64 up to this many tokens (a 128-token tile would be mostly
@@ -495,8 +441,9 @@ hipError_t launch_gemm_ring_mlp(const MlpArgs& a, int stage, hipStream_t st) {
                static_cast<uint16_t*>(a.tmp), (int)a.n, (int)a.inter, (int)a.hidden, 0, 0, nullptr, 1, nullptr};
     // 256-token tiles once there are enough of them (more reuse of each
     // weight tile), 128 below
-    static const int wr = ring_env_wr("TINYINFER_RING_WR_GU");
-    static const int nw = ring_env_nw("TINYINFER_RING_NW_GU");
+    // wave layout and waves per workgroup (tuning options; 4 x 2 and 8 by default)
+    const int wr = option(kOptRingWrGu);
+    const int nw = option(kOptRingNwGu);
     hipError_t e;
     if (nw == 4) e = wr == 2 ? launch_ring<2, 128, 2, 4>(r, st) : launch_ring<2, 128, 4, 4>(r, st);
     else if (a.n > 1024) e = wr == 2 ? launch_ring<2, 256, 2>(r, st) : launch_ring<2, 256, 4>(r, st);
@@ -508,15 +455,13 @@ hipError_t launch_gemm_ring_mlp(const MlpArgs& a, int stage, hipStream_t st) {
     RingArgs r{static_cast<const uint16_t*>(a.tmp), {a.down, a.down}, {a.down_scale, a.down_scale},
                static_cast<uint16_t*>(a.out), (int)a.n, (int)a.hidden, (int)a.inter, 0, 0, nullptr, 1,
                static_cast<const uint16_t*>(a.residual)};
-    static const int wr = ring_env_wr("TINYINFER_RING_WR_DN");
-    static const int nw = ring_env_nw("TINYINFER_RING_NW_DN");
+    const int wr = option(kOptRingWrDn);
+    const int nw = option(kOptRingNwDn);
     if (nw == 4) return wr == 2 ? launch_ring<1, 64, 2, 4>(r, st) : launch_ring<1, 64, 4, 4>(r, st);
     if (a.n <= kSmallTile) return launch_ring<1, 64, 4>(r, st);
     return wr == 2 ? launch_ring<1, 128, 2>(r, st) : launch_ring<1, 128, 4>(r, st);
   }
   return hipSuccess;
 }
-
-float* gemm_split_workspace(size_t bytes, hipStream_t st) { return split_workspace(bytes, st); }
 
 }  // namespace tinyinfer

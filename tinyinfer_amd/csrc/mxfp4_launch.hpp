@@ -31,6 +31,44 @@ struct MlpArgs {
   void* xn = nullptr;
 };
 
+// Properties of the current device, read once per device (thread-safe);
+// cus == 0 when they could not be read.
+struct DeviceInfo {
+  int cus = 0;
+  int64_t lds_per_block = 0;
+  bool gfx950 = false;
+};
+DeviceInfo device_info();
+
+// Tuning options.  Each starts from the environment variable of the same
+// name (read once, at the first query, by whichever thread gets there) and
+// can be changed at any time through set_option (the C ABI's
+// tinyinfer_mxfp4_set_option); reads and writes are atomic.
+enum Opt : int {
+  kOptRowstream,        // TINYINFER_ROWSTREAM      1: row-streaming kernels on (0 off)
+  kOptRowpair,          // TINYINFER_ROWPAIR        1: row-pair kernels on
+  kOptTile,             // TINYINFER_TILE           1: split-K tile kernels on
+  kOptTileGu,           // TINYINFER_TILE_GU        1: one-launch tile gate_up on
+  kOptRowSplitGateUp,   // TINYINFER_ROW_SPLIT_GATEUP  waves per gate_up row (0 auto, 1, 2, 4)
+  kOptRowSplitDown,     // TINYINFER_ROW_SPLIT_DOWN    waves per down row (0 auto, 1, 2, 4)
+  kOptGemmRing,         // TINYINFER_GEMM_RING      1: ring GEMM on (0: register-staged GEMM)
+  kOptRingKsplit,       // TINYINFER_RING_KSPLIT    K ranges of the ring GEMM (0 auto)
+  kOptRingWrGu,         // TINYINFER_RING_WR_GU     ring wave rows, gate_up (2 or 4)
+  kOptRingNwGu,         // TINYINFER_RING_NW_GU     ring waves per workgroup, gate_up (4 or 8)
+  kOptRingWrDn,         // TINYINFER_RING_WR_DN
+  kOptRingNwDn,         // TINYINFER_RING_NW_DN
+  kOptSkinnyNw,         // TINYINFER_SKINNY_NW      skinny waves per workgroup (0 auto, 4, 8)
+  kOptStreamSpuGu,      // TINYINFER_STREAM_SPU_GU  stream segments per unit, gate_up (0 auto)
+  kOptStreamSpuDn,      // TINYINFER_STREAM_SPU_DN
+  kOptStreamXreg,       // TINYINFER_STREAM_XREG    1: gate_up activations in VGPRs
+  kOptWorkspaceMB,      // TINYINFER_WORKSPACE_MB   limit of one split-K workspace buffer
+  kOptDecodeSpin,       // TINYINFER_DECODE_SPIN    fused decode kernel's wait bound (poll rounds)
+  kOptCount
+};
+int option(Opt o);
+bool set_option(const char* name, int value);
+bool get_option(const char* name, int* value);
+
 // Which part of the MLP a launcher runs: the gate_up stage (tmp = SiLU(x G^T) *
 // (x U^T)), the down stage (out = tmp D^T), or both in order.
 enum Stage : int { kStageGateUp = 1, kStageDown = 2, kStageBoth = 3 };
@@ -84,19 +122,28 @@ bool tile_enabled();
 bool tile_supported(const MlpArgs& a, int stage, hipStream_t stream);
 hipError_t launch_tile_mlp(const MlpArgs& a, int stage, hipStream_t stream);
 
-// The split-K workspace of the prefill GEMM: one fp32 buffer per (device,
-// stream), grown on demand, never freed; null when it cannot grow (graph
-// capture, allocation failure).
+// The split-K workspace of the GEMM and tile kernels: one fp32 buffer per
+// (device, stream), grown on demand up to workspace_limit() bytes; null when
+// it cannot grow (over the limit, graph capture, allocation failure).
+// Buffers live until release_workspaces(), which synchronizes every device
+// that holds one and frees them all.
 float* gemm_split_workspace(size_t bytes, hipStream_t stream);
+size_t workspace_limit();
+size_t workspace_bytes_held();
+hipError_t release_workspaces();
 
 // Fused decode kernel (gate_up, cross-workgroup flags, down in one launch)
 // for n <= 4 tokens; hipErrorNotSupported when the shape, alignment or the
 // device's LDS/occupancy do not allow it.
 hipError_t launch_decode_mlp(const MlpArgs& a, hipStream_t stream);
 
-// Spin timeouts of the fused decode kernel's wait since load (0 unless a
-// workgroup was not resident); synchronous.
+// Spin timeouts of the fused decode kernel's wait since load or the last
+// decode_reset() (0 unless a workgroup was not resident); synchronous.  While
+// it is nonzero, fused decode launches exit at entry without writing.
 unsigned int decode_barrier_timeouts();
+// Clears the fused decode kernel's flags, epoch, poison and timeout count on
+// the current device after synchronizing it.
+hipError_t decode_reset();
 
 // RMSNorm of n rows of `hidden` activations (the reference's rmsnorm
 // kernel, tinyinfer/csrc/rmsnorm.cu:10-54): out = round(w * x * rsqrt(sum(x^2)

@@ -372,18 +372,7 @@ __global__ __launch_bounds__(kPThreads, 1) void rowpair_kernel(PairArgs a) {
   }
 }
 
-int pair_cus() {
-  static int cache[64];
-  static bool init[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (!init[dev]) {
-    hipDeviceProp_t prop;
-    cache[dev] = hipGetDeviceProperties(&prop, dev) == hipSuccess ? prop.multiProcessorCount : 0;
-    init[dev] = true;
-  }
-  return cache[dev];
-}
+int pair_cus() { return device_info().cus; }
 
 // Waves per pair S and chunks per wave UC: gate_up whole pairs where the
 // chunks fit (4 at one pass, 3 at two), down at most 3 chunks per wave where
@@ -494,10 +483,7 @@ bool aligned16_pair(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15
 
 }  // namespace
 
-bool rowpair_enabled() {
-  const char* e = std::getenv("TINYINFER_ROWPAIR");
-  return !(e && e[0] == '0' && e[1] == '\0');
-}
+bool rowpair_enabled() { return option(kOptRowpair) != 0; }
 
 bool rowpair_supported(const MlpArgs& m, int stage) {
   if (m.dtype != kBF16) return false;

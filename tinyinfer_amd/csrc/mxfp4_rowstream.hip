@@ -420,26 +420,10 @@ __global__ __launch_bounds__(kRThreads, 1) void rowstream_kernel(RowArgs a) {
   }
 }
 
-int row_cus() {
-  static int cache[64];
-  static bool init[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (!init[dev]) {
-    hipDeviceProp_t prop;
-    cache[dev] = hipGetDeviceProperties(&prop, dev) == hipSuccess ? prop.multiProcessorCount : 0;
-    init[dev] = true;
-  }
-  return cache[dev];
-}
+int row_cus() { return device_info().cus; }
 
 bool aligned16_ptr(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-int split_env(const char* name) {
-  const char* e = std::getenv(name);
-  const int v = e ? std::atoi(e) : 0;
-  return v == 1 || v == 2 || v == 4 ? v : 0;
-}
 
 // Waves per row S and chunks per wave UC for a stage: S in {1, 2, 4} (gate_up
 // 1, 2) so that the largest share fits the VGPR budget (gate_up 4 chunks: two
@@ -461,7 +445,7 @@ bool row_plan(int64_t M, int64_t K, int64_t R, bool gateup, bool norm, int dtype
   const int ucmax = dtype != kBF16 ? 3 : M == 2 ? (gateup ? 2 : 3) : gateup ? 4 : kMaxUC;
   const int smax = gateup ? 2 : 4;
   S = 0;
-  const int want = split_env(gateup ? "TINYINFER_ROW_SPLIT_GATEUP" : "TINYINFER_ROW_SPLIT_DOWN");
+  const int want = option(gateup ? kOptRowSplitGateUp : kOptRowSplitDown);
   if (want && want <= smax && (nc + want - 1) / want <= ucmax && want <= nc) S = want;
   // down: at most 3 chunks per wave where the split allows it (8B down, 6
   // chunks: 3 + 3 measured 6.36 us against 7.38 us whole and 7.22 us over four
@@ -560,10 +544,7 @@ hipError_t row_stage(const MlpArgs& m, hipStream_t st) {
 
 }  // namespace
 
-bool rowstream_enabled() {
-  const char* e = std::getenv("TINYINFER_ROWSTREAM");
-  return !(e && e[0] == '0' && e[1] == '\0');
-}
+bool rowstream_enabled() { return option(kOptRowstream) != 0; }
 
 bool rowstream_supported(const MlpArgs& m, int stage) {
   if (m.n < 1 || m.n > 2 || (m.dtype != kBF16 && m.dtype != kF16)) return false;

@@ -259,16 +259,9 @@ void launch_one(const uint16_t* x, const uint8_t* w0, const uint8_t* s0, const u
   skinny_kernel<DT, T, NCH, GATEUP, NW><<<grid, NW * 64, 0, st>>>(x, w0, s0, w1, s1, M, K, R, out, res);
 }
 
-// Test/tuning override: TINYINFER_SKINNY_NW=<4|8> forces the waves per
-// workgroup (read once per process).
-int forced_nw() {
-  static const int v = [] {
-    const char* e = std::getenv("TINYINFER_SKINNY_NW");
-    const int n = e ? std::atoi(e) : 0;
-    return (n == 4 || n == 8) ? n : 0;
-  }();
-  return v;
-}
+// Test/tuning override: the option TINYINFER_SKINNY_NW=<4|8> forces the
+// waves per workgroup (0: chosen below).
+int forced_nw() { return option(kOptSkinnyNw); }
 
 // Waves per workgroup (4 or 8; 16 would cap registers at 128 and spill).
 // 4 when each wave's K slice fits one NCH batch and the grid still has

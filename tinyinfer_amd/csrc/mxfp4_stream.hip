@@ -520,30 +520,15 @@ struct DevCaps {
 };
 
 DevCaps caps() {
-  static DevCaps cache[64];
-  static bool init[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return DevCaps{};
-  if (!init[dev]) {
-    hipDeviceProp_t prop;
-    DevCaps d;
-    if (hipGetDeviceProperties(&prop, dev) == hipSuccess) {
-      d.cus = prop.multiProcessorCount;
-      d.max_lds = (int64_t)prop.sharedMemPerBlock;
-    }
-    cache[dev] = d;
-    init[dev] = true;
-  }
-  return cache[dev];
+  const DeviceInfo i = device_info();
+  DevCaps d;
+  d.cus = i.cus;
+  d.max_lds = i.lds_per_block;
+  return d;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-int env_int(const char* name, int dflt, int lo, int hi) {
-  const char* e = std::getenv(name);
-  const int v = e ? std::atoi(e) : dflt;
-  return v < lo ? lo : (v > hi ? hi : v);
-}
 
 // Segments per unit for a wave run of up to `spw` segments: the least of
 // load slots (units x segments per unit, the last unit padded) plus 0.8 slot
@@ -553,9 +538,7 @@ int env_int(const char* name, int dflt, int lo, int hi) {
 // segments per wave): one 3-segment unit beats a 2 + 1 split by 17%.
 // TINYINFER_STREAM_SPU_GU / _DN override it for tuning.
 int stream_spu(bool gateup, bool bf16, int spw) {
-  static const int gu = env_int("TINYINFER_STREAM_SPU_GU", 0, 0, 3);
-  static const int dn = env_int("TINYINFER_STREAM_SPU_DN", 0, 0, 4);
-  const int forced = gateup ? gu : dn;
+  const int forced = option(gateup ? kOptStreamSpuGu : kOptStreamSpuDn);
   if (forced > 0) return gateup && !bf16 && forced > 2 ? 2 : forced;
   const int cap = gateup ? (bf16 ? 3 : 2) : 4;
   int best = 1;
@@ -575,8 +558,7 @@ constexpr int kDepth = 2;         // units in flight per wave
 
 // Activations in registers for gate_up (TINYINFER_STREAM_XREG=0 turns it off).
 bool stream_xreg_allowed(bool gateup) {
-  static const int v = env_int("TINYINFER_STREAM_XREG", 1, 0, 1);
-  return v == 1 && gateup;
+  return option(kOptStreamXreg) == 1 && gateup;
 }
 
 // Geometry of one stage; false when the streaming kernel does not apply.
@@ -691,13 +673,19 @@ hipError_t run_stage(const uint16_t* x, const uint8_t* w0, const uint8_t* s0, co
 // never reset: a launch reads the epoch E, waits for flag == E + 1, and
 // workgroup 0 stores E + 1 as the new epoch after its own wait (by then every
 // workgroup has read E).  The wait is a bounded spin: if it ever gives up
-// (workgroups not all resident), the timeout is counted and the launch's
-// results are invalid, but the kernel ends.  Launches must not overlap on a
-// device.
+// (workgroups not all resident), the timeout is counted, the launch's
+// results are invalid, but the kernel ends; the wait also sets a sticky
+// poison word, so a workgroup that starts late, and every later launch,
+// exits at entry without writing anything (a late workgroup would otherwise
+// read the advanced epoch and publish a flag the next launch takes for its
+// own) until decode_reset() clears the state.  Launches must not overlap on
+// a device.
 constexpr int kFusedMaxGrid = 1024;
 constexpr int kFusedMaxUnits2 = 4;
 __device__ uint32_t g_fused_flags[kFusedMaxGrid];
-__device__ uint32_t g_fused_epoch;
+// [0] epoch of the last completed launch, [1] poisoned (nonzero after a wait
+// gave up): read together as one 64-bit word at kernel entry
+__device__ __attribute__((aligned(8))) uint32_t g_fused_ctl[2];
 __device__ uint32_t g_fused_timeouts;
 
 struct FusedArgs {
@@ -752,7 +740,12 @@ __global__ __launch_bounds__(kNW * 64, 1) void fused_kernel(FusedArgs f) {
   const int G = gridDim.x;
   const int g = blockIdx.x;
   const int q8 = lane >> 3;
-  const uint32_t epoch = __builtin_amdgcn_readfirstlane(agent_load(&g_fused_epoch));
+  const uint64_t ctl = __hip_atomic_load(reinterpret_cast<const uint64_t*>(g_fused_ctl), __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+  // after a wait that gave up, every later launch leaves its outputs alone
+  // (the flags can no longer be trusted) until the host resets the state
+  if (__builtin_amdgcn_readfirstlane((uint32_t)(ctl >> 32)) != 0u) return;
+  const uint32_t epoch = __builtin_amdgcn_readfirstlane((uint32_t)ctl);
 
   // phase 1 LDS (x, scales, partials, counters, outputs) from 0; phase 2's
   // scale rows at B.lds_scl (past both phases' other areas); phase 2's x (h),
@@ -951,7 +944,11 @@ __global__ __launch_bounds__(kNW * 64, 1) void fused_kernel(FusedArgs f) {
       for (int i = lane; i < G; i += 64) done = done && agent_load(&g_fused_flags[i]) == want;
       if (wave_all(done)) break;
       if (it >= f.spin_limit) {
-        if (lane == 0) __hip_atomic_fetch_add(&g_fused_timeouts, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) {
+          __hip_atomic_fetch_add(&g_fused_timeouts, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(&g_fused_ctl[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         break;
       }
       __builtin_amdgcn_s_sleep(1);
@@ -963,7 +960,7 @@ __global__ __launch_bounds__(kNW * 64, 1) void fused_kernel(FusedArgs f) {
   }
   __syncthreads();
   if (g == 0 && threadIdx.x == 0)
-    __hip_atomic_store(&g_fused_epoch, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&g_fused_ctl[0], epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   // h [M, I] -> LDS rows of B.xs_stride bytes, 8-byte agent-scope loads
   {
@@ -1052,7 +1049,7 @@ bool plan_fused(const MlpArgs& m, const DevCaps& d, FusedArgs& f, int& grid, int
   B.lds_scl = (int)(((p1 > p2 ? p1 : p2) + 15) & ~int64_t(15));
   lds = B.lds_scl + (int64_t)B.nrg_max * 8 * B.ss_stride;
   if (lds > d.max_lds) return false;
-  f.spin_limit = 1u << 20;
+  f.spin_limit = (uint32_t)option(kOptDecodeSpin);
   return true;
 }
 
@@ -1165,6 +1162,17 @@ unsigned int decode_barrier_timeouts() {
   unsigned int v = 0;
   if (hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_fused_timeouts), sizeof(v)) != hipSuccess) return 0xffffffffu;
   return v;
+}
+
+hipError_t decode_reset() {
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return e;
+  static const uint32_t zeros[kFusedMaxGrid] = {};
+  e = hipMemcpyToSymbol(HIP_SYMBOL(g_fused_flags), zeros, sizeof(zeros));
+  if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(g_fused_ctl), zeros, 2 * sizeof(uint32_t));
+  if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(g_fused_timeouts), zeros, sizeof(uint32_t));
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  return e;
 }
 
 }  // namespace tinyinfer

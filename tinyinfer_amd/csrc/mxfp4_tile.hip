@@ -334,18 +334,7 @@ __global__ __launch_bounds__(kTThreads, 1) void tile_gu_kernel(TileArgs a, uint1
   }
 }
 
-int tile_cus() {
-  static int cache[64];
-  static bool init[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (!init[dev]) {
-    hipDeviceProp_t prop;
-    cache[dev] = hipGetDeviceProperties(&prop, dev) == hipSuccess ? prop.multiProcessorCount : 0;
-    init[dev] = true;
-  }
-  return cache[dev];
-}
+int tile_cus() { return device_info().cus; }
 
 // Workgroups per K range: about one workgroup per CU over all ranges, at
 // least one group per wave, then as few as give every wave the same largest
@@ -396,10 +385,7 @@ bool tile_gu_fits(const TileArgs& a, int mt) {
   return (S == 1 || S == 2 || S == 4) && mt <= 2 && mt * S <= 4 && a.R % 16 == 0;
 }
 
-bool tile_gu_enabled() {
-  const char* e = std::getenv("TINYINFER_TILE_GU");
-  return !(e && e[0] == '0' && e[1] == '\0');
-}
+bool tile_gu_enabled() { return option(kOptTileGu) != 0; }
 
 template <int MT, int S>
 hipError_t tile_gu_launch(const TileArgs& a, int grid, uint16_t* out, hipStream_t st) {
@@ -464,10 +450,7 @@ hipError_t tile_stage(const MlpArgs& m, hipStream_t st) {
 
 }  // namespace
 
-bool tile_enabled() {
-  const char* e = std::getenv("TINYINFER_TILE");
-  return !(e && e[0] == '0' && e[1] == '\0');
-}
+bool tile_enabled() { return option(kOptTile) != 0; }
 
 bool tile_supported(const MlpArgs& m, int stage, hipStream_t st) {
   if (m.dtype != kBF16) return false;
