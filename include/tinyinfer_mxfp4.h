@@ -47,6 +47,7 @@ extern "C" {
 #define TI_ERR_TOO_LARGE 6        /* a size exceeds what the kernels index */
 #define TI_ERR_MISALIGNED 7       /* X, gate, up, down or tmp not 16-byte aligned */
 #define TI_ERR_UNSUPPORTED 8      /* a forced kernel path cannot run this call */
+#define TI_ERR_SCRATCH 9          /* the no-alloc entry point's fixed scratch is too small for the call */
 
 /* dtype codes: the reference's dtype_code values (mlp_fp4.cu:481-515), plus fp32. */
 #define TI_DTYPE_F16 0
@@ -84,6 +85,26 @@ int tinyinfer_mlp_forward_mxfp4(const void* X, const uint8_t* gate, const uint8_
                                 const uint8_t* down_scale, size_t N, size_t hidden_dim,
                                 size_t intermediate, void* tmp, void* O, int dtype_code,
                                 void* stream);
+
+/*
+ * tinyinfer_mlp_forward_mxfp4 without any device allocation. No counterpart
+ * in the reference: it is for callers that cannot allocate (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, kernels and results as tinyinfer_mlp_forward_mxfp4; the
+ * split-K partial sums go to a fixed 64 MiB device array of the library (one
+ * per device, held until the process ends) instead of an allocated
+ * workspace, and no hipMalloc/hipFree is called.  A call whose split-K tile
+ * kernels would need more than 64 MiB (far beyond the Qwen3 MLP shapes) is
+ * refused with TI_ERR_SCRATCH; the GEMM path splits K only as far as the
+ * array holds.  All calls on one device share its array: calls that overlap
+ * on a device (other streams or threads, concurrent graph replays) race and
+ * must not run at the same time.
+ */
+int tinyinfer_mlp_forward_mxfp4_noalloc(const void* X, const uint8_t* gate, const uint8_t* gate_scale,
+                                        const uint8_t* up, const uint8_t* up_scale, const uint8_t* down,
+                                        const uint8_t* down_scale, size_t N, size_t hidden_dim,
+                                        size_t intermediate, void* tmp, void* O, int dtype_code,
+                                        void* stream);
 
 /*
  * Same as tinyinfer_mlp_forward_mxfp4 with the kernel path forced

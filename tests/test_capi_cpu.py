@@ -48,7 +48,7 @@ def test_python_constants_match_header(capi):
 
 
 def test_abi_version_and_status_strings(capi):
-    assert capi.lib().tinyinfer_mxfp4_abi_version() == 6
+    assert capi.lib().tinyinfer_mxfp4_abi_version() == 7
     assert capi.status_string(0) == "ok"
     assert "32" in capi.status_string(capi.TI_ERR_BAD_SHAPE)
     assert capi.status_string(999) == "unknown status"

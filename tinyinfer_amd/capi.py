@@ -23,6 +23,7 @@ TI_ERR_NO_DEVICE = 5
 TI_ERR_TOO_LARGE = 6
 TI_ERR_MISALIGNED = 7
 TI_ERR_UNSUPPORTED = 8
+TI_ERR_SCRATCH = 9
 
 TI_DTYPE_F16 = 0
 TI_DTYPE_BF16 = 1
@@ -40,6 +41,8 @@ TI_QFLAG_EXP_RANGE = 2
 _vp, _u8p, _sz, _int = ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
 SIGNATURES = {
     "tinyinfer_mlp_forward_mxfp4": (_int, [_vp, _u8p, _u8p, _u8p, _u8p, _u8p, _u8p, _sz, _sz, _sz, _vp, _vp, _int, _vp]),
+    "tinyinfer_mlp_forward_mxfp4_noalloc": (_int, [_vp, _u8p, _u8p, _u8p, _u8p, _u8p, _u8p, _sz, _sz, _sz, _vp, _vp, _int,
+                                                   _vp]),
     "tinyinfer_mlp_forward_mxfp4_path": (_int, [_vp, _u8p, _u8p, _u8p, _u8p, _u8p, _u8p, _sz, _sz, _sz, _vp, _vp, _int, _int, _vp]),
     "tinyinfer_mlp_gate_up_mxfp4": (_int, [_vp, _u8p, _u8p, _u8p, _u8p, _sz, _sz, _sz, _vp, _int, _int, _vp]),
     "tinyinfer_mlp_down_mxfp4": (_int, [_vp, _u8p, _u8p, _sz, _sz, _sz, _vp, _int, _int, _vp]),

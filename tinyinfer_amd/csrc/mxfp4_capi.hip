@@ -6,6 +6,7 @@
 // instead of thrown exceptions, so the boundary is safe for any FFI.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 
 #include "../../include/tinyinfer_mxfp4.h"
 #include "mxfp4_common.hpp"
@@ -88,6 +89,15 @@ int mlp_impl(const MlpArgs& a, int stage, int path, void* stream) {
   st = check_device();
   if (st != TI_OK) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // a caller-provided workspace (the no-alloc entry point) must hold the
+  // whole split of the tile kernels when they would run
+  if (a.ws && (path == TI_PATH_AUTO || path == TI_PATH_SKINNY) && (size_t)a.n <= kTileMaxTokens &&
+      tinyinfer::tile_enabled()) {
+    size_t need = 0;
+    for (int sg : {(int)tinyinfer::kStageGateUp, (int)tinyinfer::kStageDown})
+      if (stage & sg) need = std::max(need, tinyinfer::tile_workspace_need(a, sg));
+    if (need > a.ws_bytes) return TI_ERR_SCRATCH;
+  }
   if (path == TI_PATH_DECODE) {
     if (stage != tinyinfer::kStageBoth) return TI_ERR_UNSUPPORTED;
     const hipError_t e = tinyinfer::launch_decode_mlp(a, s);
@@ -115,6 +125,8 @@ int mlp_impl(const MlpArgs& a, int stage, int path, void* stream) {
 int64_t as_dim(size_t v) { return v > (size_t)INT64_MAX ? -1 : (int64_t)v; }
 
 }  // namespace
+
+int tinyinfer::run_mlp(const MlpArgs& a, int stage, int path, void* stream) { return mlp_impl(a, stage, path, stream); }
 
 extern "C" {
 
@@ -272,6 +284,7 @@ const char* tinyinfer_mxfp4_status_string(int status) {
     case TI_ERR_TOO_LARGE: return "size exceeds kernel limits";
     case TI_ERR_MISALIGNED: return "activation, weight and tmp pointers must be 16-byte aligned";
     case TI_ERR_UNSUPPORTED: return "the requested kernel path does not support this call";
+    case TI_ERR_SCRATCH: return "the call needs more scratch memory than the no-alloc entry point's fixed buffer holds";
     default: return "unknown status";
   }
 }
@@ -309,6 +322,6 @@ int tinyinfer_mxfp4_workspace_info(size_t* bytes_held, size_t* limit_bytes) {
 
 int tinyinfer_mxfp4_release_workspaces(void) { return to_status(tinyinfer::release_workspaces()); }
 
-int tinyinfer_mxfp4_abi_version(void) { return 6; }
+int tinyinfer_mxfp4_abi_version(void) { return 7; }
 
 }  // extern "C"

@@ -361,11 +361,11 @@ __global__ __launch_bounds__(256) void ring_reduce(const float* __restrict__ ws,
 // launch.  The smallest split with the least cost wins; K ranges are whole
 // 8-step blocks, and the partials of all ranges fit the workspace limit.
 // The option TINYINFER_RING_KSPLIT=<n> forces n (clamped), for tuning.
-int ring_ksplit(const RingArgs& r, int bm, int nmat, int64_t tiles, int per_cu) {
+int ring_ksplit(const RingArgs& r, int bm, int nmat, int64_t tiles, int per_cu, size_t ws_limit) {
   const int nblk = r.K / (8 * kBK);
   int cap = nblk < 32 ? nblk : 32;
   const size_t per_split = (size_t)r.M * nmat * r.N * sizeof(float);
-  const size_t fit = per_split ? workspace_limit() / per_split : 0;
+  const size_t fit = per_split ? ws_limit / per_split : 0;
   if ((size_t)cap > fit) cap = (int)fit;
   if (cap < 2) return 1;
   if (const int v = option(kOptRingKsplit); v >= 1) return v < cap ? v : cap;
@@ -386,18 +386,28 @@ int ring_ksplit(const RingArgs& r, int bm, int nmat, int64_t tiles, int per_cu) 
   return best;
 }
 
+// A caller-provided workspace (fixed != null) of fixed_bytes is used instead
+// of the library's per-stream one, and nothing is allocated.
+struct FixedWs {
+  float* ptr;
+  size_t bytes;
+};
+
 template <int NMAT, int BM, int WR, int NW = 8>
-hipError_t launch_ring(RingArgs r, hipStream_t st) {
+hipError_t launch_ring(RingArgs r, hipStream_t st, FixedWs fixed) {
   using C = RingCfg<BM, NW>;
   constexpr int kRowsOut = NMAT == 2 ? 128 : 256;
   r.m_tiles = (r.M + BM - 1) / BM;
   r.n_tiles = (r.N + kRowsOut - 1) / kRowsOut;
   const int64_t tiles = (int64_t)r.m_tiles * r.n_tiles;
   if (tiles > 0x7fffffff / 32) return hipErrorInvalidValue;
-  const int ksplit_want = ring_ksplit(r, BM, NMAT, tiles, NW == 4 ? 2 : 1);
+  const int ksplit_want =
+      ring_ksplit(r, BM, NMAT, tiles, NW == 4 ? 2 : 1, fixed.ptr ? fixed.bytes : workspace_limit());
   int ksplit = 1;
+  r.ws = nullptr;
   if (ksplit_want > 1) {
-    r.ws = gemm_split_workspace((size_t)ksplit_want * r.M * NMAT * r.N * sizeof(float), st);
+    r.ws = fixed.ptr ? fixed.ptr
+                     : gemm_split_workspace((size_t)ksplit_want * r.M * NMAT * r.N * sizeof(float), st);
     if (r.ws) ksplit = ksplit_want;
   }
   r.ksplit = ksplit;
@@ -436,6 +446,7 @@ bool gemm_ring_supported(const MlpArgs& a, int stage) {
 constexpr int64_t kSmallTile = 64;
 
 hipError_t launch_gemm_ring_mlp(const MlpArgs& a, int stage, hipStream_t st) {
+  const FixedWs fx{a.ws, a.ws_bytes};
   if (stage & kStageGateUp) {
     RingArgs r{static_cast<const uint16_t*>(a.x), {a.gate, a.up}, {a.gate_scale, a.up_scale},
                static_cast<uint16_t*>(a.tmp), (int)a.n, (int)a.inter, (int)a.hidden, 0, 0, nullptr, 1, nullptr};
@@ -445,10 +456,10 @@ hipError_t launch_gemm_ring_mlp(const MlpArgs& a, int stage, hipStream_t st) {
     const int wr = option(kOptRingWrGu);
     const int nw = option(kOptRingNwGu);
     hipError_t e;
-    if (nw == 4) e = wr == 2 ? launch_ring<2, 128, 2, 4>(r, st) : launch_ring<2, 128, 4, 4>(r, st);
-    else if (a.n > 1024) e = wr == 2 ? launch_ring<2, 256, 2>(r, st) : launch_ring<2, 256, 4>(r, st);
-    else if (a.n <= kSmallTile) e = launch_ring<2, 64, 4>(r, st);
-    else e = wr == 2 ? launch_ring<2, 128, 2>(r, st) : launch_ring<2, 128, 4>(r, st);
+    if (nw == 4) e = wr == 2 ? launch_ring<2, 128, 2, 4>(r, st, fx) : launch_ring<2, 128, 4, 4>(r, st, fx);
+    else if (a.n > 1024) e = wr == 2 ? launch_ring<2, 256, 2>(r, st, fx) : launch_ring<2, 256, 4>(r, st, fx);
+    else if (a.n <= kSmallTile) e = launch_ring<2, 64, 4>(r, st, fx);
+    else e = wr == 2 ? launch_ring<2, 128, 2>(r, st, fx) : launch_ring<2, 128, 4>(r, st, fx);
     if (e != hipSuccess) return e;
   }
   if (stage & kStageDown) {
@@ -457,9 +468,9 @@ hipError_t launch_gemm_ring_mlp(const MlpArgs& a, int stage, hipStream_t st) {
                static_cast<const uint16_t*>(a.residual)};
     const int wr = option(kOptRingWrDn);
     const int nw = option(kOptRingNwDn);
-    if (nw == 4) return wr == 2 ? launch_ring<1, 64, 2, 4>(r, st) : launch_ring<1, 64, 4, 4>(r, st);
-    if (a.n <= kSmallTile) return launch_ring<1, 64, 4>(r, st);
-    return wr == 2 ? launch_ring<1, 128, 2>(r, st) : launch_ring<1, 128, 4>(r, st);
+    if (nw == 4) return wr == 2 ? launch_ring<1, 64, 2, 4>(r, st, fx) : launch_ring<1, 64, 4, 4>(r, st, fx);
+    if (a.n <= kSmallTile) return launch_ring<1, 64, 4>(r, st, fx);
+    return wr == 2 ? launch_ring<1, 128, 2>(r, st, fx) : launch_ring<1, 128, 4>(r, st, fx);
   }
   return hipSuccess;
 }

@@ -29,6 +29,11 @@ struct MlpArgs {
   const void* norm_w = nullptr;   // [hidden] activation dtype
   float eps = 0.f;
   void* xn = nullptr;
+  // Caller-provided split-K workspace (the no-alloc entry point): when ws is
+  // set, the tile and GEMM launchers use it, up to ws_bytes, and never
+  // allocate; null: the per-(device, stream) buffer of gemm_split_workspace.
+  float* ws = nullptr;
+  size_t ws_bytes = 0;
 };
 
 // Properties of the current device, read once per device (thread-safe);
@@ -120,6 +125,9 @@ hipError_t launch_rowpair_mlp(const MlpArgs& a, int stage, hipStream_t stream);
 // false when TINYINFER_TILE=0.
 bool tile_enabled();
 bool tile_supported(const MlpArgs& a, int stage, hipStream_t stream);
+// Workspace bytes the tile kernels need for this call, 0 when they do not
+// apply (shape, dtype, alignment).
+size_t tile_workspace_need(const MlpArgs& a, int stage);
 hipError_t launch_tile_mlp(const MlpArgs& a, int stage, hipStream_t stream);
 
 // The split-K workspace of the GEMM and tile kernels: one fp32 buffer per
@@ -144,6 +152,10 @@ unsigned int decode_barrier_timeouts();
 // Clears the fused decode kernel's flags, epoch, poison and timeout count on
 // the current device after synchronizing it.
 hipError_t decode_reset();
+
+// The whole MLP entry (validation, device check, kernel choice, launches) of
+// the C ABI, returning a TI_* status; `path` is a TI_PATH_* value.
+int run_mlp(const MlpArgs& a, int stage, int path, void* stream);
 
 // RMSNorm of n rows of `hidden` activations (the reference's rmsnorm
 // kernel, tinyinfer/csrc/rmsnorm.cu:10-54): out = round(w * x * rsqrt(sum(x^2)

@@ -408,7 +408,7 @@ hipError_t tile_stage(const MlpArgs& m, hipStream_t st) {
   const int64_t K = GATEUP ? m.hidden : m.inter;
   const int64_t R = GATEUP ? m.inter : m.hidden;
   if (m.dtype != kBF16 || !tile_plan(m.n, K, R, GATEUP, a, grid, mt, bytes)) return hipErrorNotSupported;
-  a.ws = gemm_split_workspace(bytes, st);
+  a.ws = m.ws ? (bytes <= m.ws_bytes ? m.ws : nullptr) : gemm_split_workspace(bytes, st);
   if (!a.ws) return hipErrorNotSupported;
   a.x = static_cast<const uint16_t*>(GATEUP ? m.x : m.tmp);
   a.w0 = GATEUP ? m.gate : m.down;
@@ -452,27 +452,34 @@ hipError_t tile_stage(const MlpArgs& m, hipStream_t st) {
 
 bool tile_enabled() { return option(kOptTile) != 0; }
 
-bool tile_supported(const MlpArgs& m, int stage, hipStream_t st) {
-  if (m.dtype != kBF16) return false;
-  if ((stage & kStageGateUp) && m.norm_w != nullptr) return false;
+size_t tile_workspace_need(const MlpArgs& m, int stage) {
+  if (m.dtype != kBF16) return 0;
+  if ((stage & kStageGateUp) && m.norm_w != nullptr) return 0;
   TileArgs a;
   int grid = 0, mt = 0;
   size_t bytes = 0, need = 0;
   if (stage & kStageGateUp) {
-    if (!tile_plan(m.n, m.hidden, m.inter, true, a, grid, mt, bytes)) return false;
+    if (!tile_plan(m.n, m.hidden, m.inter, true, a, grid, mt, bytes)) return 0;
     need = std::max(need, bytes);
   }
   if (stage & kStageDown) {
-    if (!tile_plan(m.n, m.inter, m.hidden, false, a, grid, mt, bytes)) return false;
+    if (!tile_plan(m.n, m.inter, m.hidden, false, a, grid, mt, bytes)) return 0;
     need = std::max(need, bytes);
   }
   // 16-byte loads of activations, weights and scale runs; 8-byte output stores
   const void* p16[] = {m.x, m.gate, m.up, m.down, m.gate_scale, m.up_scale, m.down_scale, m.tmp};
   for (const void* p : p16)
-    if (p && !aligned_tile(p, 16)) return false;
+    if (p && !aligned_tile(p, 16)) return 0;
   const void* p8[] = {m.out, m.residual};
   for (const void* p : p8)
-    if (p && !aligned_tile(p, 8)) return false;
+    if (p && !aligned_tile(p, 8)) return 0;
+  return need;
+}
+
+bool tile_supported(const MlpArgs& m, int stage, hipStream_t st) {
+  const size_t need = tile_workspace_need(m, stage);
+  if (need == 0) return false;
+  if (m.ws) return need <= m.ws_bytes;
   return gemm_split_workspace(need, st) != nullptr;
 }
 
