@@ -71,3 +71,50 @@ def test_written_checkpoint_runs(tmp_path):
         mats = [want[p + f"{proj}.weight_{kind}"] for proj in ("gate_proj", "up_proj", "down_proj")
                 for kind in ("packed", "scale")]
         assert_parity(out.cpu(), om.mlp_reference(x, *mats), f"layer {layer}")
+
+
+@pytest.mark.parametrize("tied", [False, True])
+def test_writer_attention_and_lm_head(tmp_path, tied):
+    """Opt-in groups: attention projections and lm_head (its own weight, or
+    the tied embedding) converted to the oracle's bytes, the record lists
+    them, and the converted linears loaded into the reference's module
+    layout (q/k/v merged) compute within the parity bar."""
+    from safetensors import safe_open
+    import torch.nn.functional as F
+    from tests.ckpt_helpers import module_config
+    banner(f"checkpoint attention + lm_head tied={tied}")
+    cfg = tiny_config(hidden=512, inter=1024, heads=8, kv_heads=2, vocab=2048, tied=tied)
+    src_t = hf_tensors(cfg, seed=9, full_attn=True, lm_head=not tied)
+    write_hf(tmp_path / "src", cfg, src_t, shards=2)
+    groups = ("mlp", "attn", "lm_head")
+    rep = ck.quantize_checkpoint(tmp_path / "src", tmp_path / "dst", groups=groups, chunk_rows=100,
+                                 log=lambda *_: None)
+    want = oracle_mxfp4_tensors(src_t, groups, tied=tied)
+    got = {}
+    for f in sorted((tmp_path / "dst").glob("*.safetensors")):
+        with safe_open(str(f), framework="pt", device="cpu") as r:
+            got.update({k: r.get_tensor(k) for k in r.keys()})
+    assert set(got) == set(want)
+    for k in want:
+        assert got[k].dtype == want[k].dtype and torch.equal(got[k], want[k]), k
+    assert rep["num_quantized_matrices"] == 2 * 7 + 1
+    qc = json.loads((tmp_path / "dst" / "quantization_config.json").read_text())
+    assert qc["target_modules"][-5:] == ["self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj",
+                                         "self_attn.o_proj", "lm_head"]
+    mod = ck.Qwen3MXFP4Linears(module_config(cfg), groups).to("cuda")
+    ck.load_mxfp4_weights(mod, tmp_path / "dst")
+    x = torch.randn(5, 512, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16)
+
+    def ref(base, inp):
+        w = om.dequant_weight(want[base + ".weight_packed"], want[base + ".weight_scale"], torch.bfloat16)
+        return F.linear(inp, w)
+
+    for layer in range(2):
+        a = mod.attn(layer)
+        p = f"model.layers.{layer}.self_attn."
+        q, k, v = a.qkv_proj.split_qkv(a.qkv_proj(x.cuda()))
+        for name, y in (("q", q), ("k", k), ("v", v)):
+            assert_parity(y.cpu(), ref(p + f"{name}_proj", x), f"layer {layer} {name}_proj")
+        h = torch.randn(5, 512, generator=torch.Generator().manual_seed(layer)).to(torch.bfloat16)
+        assert_parity(a.o_proj(h.cuda()).cpu(), ref(p + "o_proj", h), f"layer {layer} o_proj")
+    assert_parity(mod.lm_head(x.cuda()).cpu(), ref("lm_head", x), "lm_head")
