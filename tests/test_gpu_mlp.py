@@ -80,6 +80,13 @@ def test_config0_qwen3_0p6b_m16(capi):
     out = capi.mlp_forward(xd, *md).cpu()
     st = om.parity_stats(out, ks)
     assert st["rel_max_err"] < 5e-3 and st["cos"] > 0.99999, st
+    # and against the fp64 brute force (no intermediate rounding at all):
+    # the error every path carries from bf16 activations, h and out
+    ref64 = om.mlp_fp64(x, *mats)
+    for path, o in run_all_paths(capi, xd, md).items():
+        st64 = om.parity_stats(o, torch.from_numpy(ref64))
+        print(f"config0 vs fp64 path={path}: rel_max_err={st64['rel_max_err']:.3e} cos={st64['cos']:.7f}")
+        assert om.within_tolerance(st64), (path, st64)
 
 
 def test_config0_device_quantizer_and_output_match_golden(capi):
