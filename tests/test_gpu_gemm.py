@@ -1,12 +1,15 @@
 """GPU parity of the prefill GEMM path (TI_PATH_GEMM, and TI_PATH_AUTO at
 N >= 96): the direct-to-LDS ring kernels for bf16 activations with hidden and
-intermediate multiples of 512, the register-staged GEMM otherwise.
+intermediate multiples of 512 (bf16 and fp16), the register-staged GEMM
+otherwise.
 
 Each stage is called through its C-ABI entry point and compared with the CPU
 oracle at the kernel's rounding points (exact sums, h rounded once to the
 activation dtype): a few bf16 ulps. Cases: partial token tiles, the Qwen3
 block shapes, scale bytes outside the hardware conversion's exact range,
-fp16 activations (register-staged kernel), bit-reproducibility, and the
+fp16 activations (the ring's fp16 MFMA path, fp16-subnormal weights, and
+its exact hi + lo path for scale bytes below fp16's range),
+bit-reproducibility, and the
 split-K form of the ring kernels (fp32 partials over K ranges summed in a
 fixed order by a reduce kernel) that runs when the output tiles alone would
 leave CUs idle.""" 
@@ -89,6 +92,74 @@ def test_gemm_fp16_activations(capi):
     banner("gemm fp16")
     x, mats = make_case(130, 1024, 1536, seed=5, dtype=torch.float16)
     run_gemm_stages(capi, x, mats, "fp16")
+
+
+@pytest.mark.parametrize("h,i,m", [(4096, 12288, 256), (2048, 6144, 200), (1024, 3072, 1100)])
+def test_gemm_fp16_qwen3_shapes(capi, h, i, m):
+    """fp16 activations on the ring kernels (fp16 MFMAs on weights converted to
+    fp16, split K at 8B M=256), at the Qwen3 shapes."""
+    banner(f"gemm fp16 qwen3 h={h} i={i} m={m}")
+    x, mats = make_case(m, h, i, seed=h + m + 1, dtype=torch.float16)
+    run_gemm_stages(capi, x, mats, f"fp16 h={h} i={i} m={m}")
+
+
+def _isolate_block(dp, ds, rows, blk, byte):
+    """Down rows whose only nonzero weights are one 32-element block with the
+    given scale byte (the other blocks keep their scale bytes, codes zero)."""
+    for row in rows:
+        dp[row, :] = 0
+        dp[row, blk * 16:(blk + 1) * 16] = (np.arange(16) * 17).astype(np.uint8)   # codes c | c << 4
+        ds[row, blk] = byte
+
+
+def _ulps_f16(a, b):
+    ia = a.view(torch.int16).to(torch.int32)
+    ib = b.view(torch.int16).to(torch.int32)
+    return (ia - ib).abs().max().item()
+
+
+def test_gemm_fp16_subnormal_weights(capi):
+    """Scale bytes 104..113 make fp16 subnormal weights on the fast path (the
+    whole tile stays on it): rows that read only such a block equal the exact
+    sum rounded to fp16 within one unit (a flush to zero would give 0)."""
+    banner("gemm fp16 subnormal weights")
+    x, mats = make_case(160, 1024, 2048, seed=93, dtype=torch.float16)
+    gp, gs, up, us, dp, ds = [np.array(a) for a in mats]
+    rows = {5: 104, 333: 107, 1000: 113}
+    for row, byte in rows.items():
+        _isolate_block(dp, ds, [row], 7, byte)
+    mats = [gp, gs, up, us, dp, ds]
+    assert ((ds >= 104) & (ds <= 140)).all() and ((gs >= 104) & (gs <= 140)).all()
+    out, ref = run_gemm_stages(capi, x, mats, "fp16 subnormal weights", cols=[c for c in range(1024) if c not in rows])
+    xd, md = to_dev(x, mats)
+    h_ref = h_semantics(x, gp, gs, up, us)
+    o = capi.down(h_ref.to("cuda"), md[4], md[5], path=GEMM).cpu()
+    o_ref = down_semantics(h_ref, dp, ds)
+    for row in rows:
+        assert o_ref[:, row].float().abs().max() > 0
+        assert _ulps_f16(o[:, row], o_ref[:, row]) <= 1, row
+
+
+def test_gemm_fp16_scales_outside_fp16_range(capi):
+    """A scale byte below 104 (weights below fp16's range) sends its tiles to
+    the exact bf16 weights against the activations' bf16 hi + lo parts: the
+    whole output within tolerance, the isolated rows exact to one unit."""
+    banner("gemm fp16 hi/lo path")
+    x, mats = make_case(160, 1024, 2048, seed=94, dtype=torch.float16)
+    gp, gs, up, us, dp, ds = [np.array(a) for a in mats]
+    gs[40, 3] = 90
+    us[1500, 20] = 95
+    rows = [9, 600]
+    _isolate_block(dp, ds, rows, 11, 103)
+    mats = [gp, gs, up, us, dp, ds]
+    run_gemm_stages(capi, x, mats, "fp16 hi/lo", cols=[c for c in range(1024) if c not in rows])
+    xd, md = to_dev(x, mats)
+    h_ref = h_semantics(x, gp, gs, up, us)
+    o = capi.down(h_ref.to("cuda"), md[4], md[5], path=GEMM).cpu()
+    o_ref = down_semantics(h_ref, dp, ds)
+    for row in rows:
+        assert o_ref[:, row].float().abs().max() > 0
+        assert _ulps_f16(o[:, row], o_ref[:, row]) <= 1, row
 
 
 def test_gemm_deterministic_and_full_call(capi):

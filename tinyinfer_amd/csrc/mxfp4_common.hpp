@@ -83,6 +83,25 @@ __device__ __forceinline__ u32x4_t dq8_bf16_fast(uint32_t w, uint32_t b) {
   return r;
 }
 
+// Scale bytes for which every e2m1 value times 2^(b-127) is exactly an fp16
+// number: the smallest, 2^(b-128), at least fp16's smallest subnormal 2^-24
+// (all values are multiples of it, with at most 4 significant bits), the
+// largest, 6 * 2^(b-127), at most 49152 < 65504.  (Kernels keep fp16
+// denormals: the code object's fp16/fp64 denormal mode preserves them.)
+__device__ __forceinline__ bool e8m0_f16_ok(uint32_t b) { return (b - 104u) <= 36u; }
+
+// dq8_f16_fast: eight codes times the block scale as fp16, by the hardware
+// conversion (v_cvt_scalef32_pk_f16_fp4); exact only when e8m0_f16_ok(b).
+__device__ __forceinline__ u32x4_t dq8_f16_fast(uint32_t w, uint32_t b) {
+  u32x4_t r;
+  const float s = __uint_as_float(b << 23);
+  r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 0));
+  r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 1));
+  r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 2));
+  r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 3));
+  return r;
+}
+
 // dq8_bf16_exact: exact for every scale byte (subnormal products, +-inf, NaN).
 __device__ __forceinline__ u32x4_t dq8_bf16_exact(uint32_t w, uint32_t b) {
   u32x4_t r;
@@ -203,6 +222,10 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c)
 __device__ __forceinline__ f32x16_t mfma32x32x16(u32x4_t a, u32x4_t b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16_t mfma32x32x16_f16(u32x4_t a, u32x4_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
 }
 
 }  // namespace tinyinfer

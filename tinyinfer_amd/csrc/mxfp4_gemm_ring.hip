@@ -116,7 +116,15 @@ __device__ __forceinline__ void tile_row(int tr, int row0, int N, int& mat, int&
 // of more conversions.
 // NW: waves per workgroup.  8 waves run one workgroup per CU; 4 waves with
 // 128-token tiles fit two workgroups per CU, whose barriers are independent.
-template <int NMAT, int BM, bool SPLIT, int WR, int NW>
+// DT: the activation dtype.  fp16 activations take one of two arithmetics,
+// chosen once per workgroup before the K loop from the tile's scale bytes
+// (a choice inside the loop, around the MFMAs, would keep two copies of the
+// accumulators): every byte in e8m0_f16_ok -> the weights converted to fp16
+// by the hardware (exact there) against the fp16 activations on fp16 MFMAs;
+// otherwise the exact bf16 weights against the activations' exact bf16 hi
+// and lo parts, two bf16 MFMAs per product (exact products either way,
+// fp32 sums).
+template <int NMAT, int BM, bool SPLIT, int WR, int NW, int DT = kBF16>
 __global__ __launch_bounds__(NW * 64, 2) void gemm_ring_kernel(RingArgs a) {
   using C = RingCfg<BM, NW>;
   constexpr int WT = NW / WR;                  // waves along the tokens
@@ -218,6 +226,29 @@ __global__ __launch_bounds__(NW * 64, 2) void gemm_ring_kernel(RingArgs a) {
   issue_stage(kbeg);
   if (kbeg + 1 < kend) issue_stage(kbeg + 1);
 
+  bool f16_fast = true;
+  if constexpr (DT == kF16) {
+    // the tile rows' scale bytes of steps [kbeg, kend): 2 per step, 16-byte
+    // runs (K / 32 and 2 kbeg are multiples of 16); the barrier also lets
+    // the two stages issued above land
+    const int runs = 2 * (kend - kbeg) / 16;
+    bool ok = true;
+    for (int i = threadIdx.x; i < kWRows * runs; i += NW * 64) {
+      const int tr = i / runs, c = i - tr * runs;
+      int mat, row;
+      tile_row<NMAT>(tr, row0, N, mat, row);
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(a.s[mat] + (int64_t)row * (K / 32) + 2 * kbeg + 16 * c);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ok = ok && e8m0_f16_ok((v[j] >> (8 * e)) & 0xffu);
+    }
+    f16_fast = __syncthreads_and(ok) != 0;
+  }
+
+  // MODE 0: bf16 activations; 1: fp16, weights as fp16; 2: fp16, hi + lo
+  auto k_loop = [&](auto mode_tag) {
+  constexpr int MODE = decltype(mode_tag)::value;
   for (int k = kbeg; k < kend; ++k) {
     // this wave's loads of stage k are done when at most stage k+1's remain
     if (k + 1 < kend) {
@@ -242,7 +273,7 @@ __global__ __launch_bounds__(NW * 64, 2) void gemm_ring_kernel(RingArgs a) {
       const int tr = wtr[b];
       wraw[b] = *reinterpret_cast<const u32x4_t*>(st + C::kXBytes + tr * 32 + 16 * (j ^ ((tr >> 3) & 1)));
       wsc[b] = sb[tr * 16 + 2 * (k & 7) + j];
-      ok = ok && e8m0_fast_ok(wsc[b]);
+      if constexpr (MODE != 1) ok = ok && e8m0_fast_ok(wsc[b]);
     }
     // X operands of MFMA k-step s, one 16-byte read per token block
     auto load_x = [&](int s, u32x4_t (&xo)[kTT]) {
@@ -258,7 +289,7 @@ __global__ __launch_bounds__(NW * 64, 2) void gemm_ring_kernel(RingArgs a) {
     // scale byte outside [2, 252], wave-uniform and rare) rewrites only the
     // two converted operands: a branch around the MFMAs themselves made the
     // compiler keep two copies of the accumulators.
-    const bool fast = wave_all(ok);
+    const bool fast = MODE == 1 || wave_all(ok);
     u32x4_t xa[kTT], xb[kTT];
     load_x(0, xa);
 #pragma unroll
@@ -267,19 +298,42 @@ __global__ __launch_bounds__(NW * 64, 2) void gemm_ring_kernel(RingArgs a) {
       u32x4_t (&xn)[kTT] = (s & 1) ? xa : xb;
       if (s < 3) load_x(s + 1, xn);
       u32x4_t wop[WB];
+      if constexpr (MODE == 1) {
 #pragma unroll
-      for (int b = 0; b < WB; ++b) wop[b] = dq8_bf16_fast(wraw[b][s], wsc[b]);
-      if (!fast) {
+        for (int b = 0; b < WB; ++b) wop[b] = dq8_f16_fast(wraw[b][s], wsc[b]);
 #pragma unroll
-        for (int b = 0; b < WB; ++b) wop[b] = dq8_bf16_exact(wraw[b][s], wsc[b]);
+        for (int b = 0; b < WB; ++b)
+#pragma unroll
+          for (int t = 0; t < kTT; ++t) acc[b][t] = mfma32x32x16_f16(wop[b], xc[t], acc[b][t]);
+      } else {
+#pragma unroll
+        for (int b = 0; b < WB; ++b) wop[b] = dq8_bf16_fast(wraw[b][s], wsc[b]);
+        if (!fast) {
+#pragma unroll
+          for (int b = 0; b < WB; ++b) wop[b] = dq8_bf16_exact(wraw[b][s], wsc[b]);
+        }
+        if constexpr (MODE == 2) {
+#pragma unroll
+          for (int t = 0; t < kTT; ++t) {
+            u32x4_t xh, xl;
+            f16x8_split_bf16(xc[t], xh, xl);
+#pragma unroll
+            for (int b = 0; b < WB; ++b) acc[b][t] = mfma32x32x16(wop[b], xl, mfma32x32x16(wop[b], xh, acc[b][t]));
+          }
+        } else {
+#pragma unroll
+          for (int b = 0; b < WB; ++b)
+#pragma unroll
+            for (int t = 0; t < kTT; ++t) acc[b][t] = mfma32x32x16(wop[b], xc[t], acc[b][t]);
+        }
       }
-#pragma unroll
-      for (int b = 0; b < WB; ++b)
-#pragma unroll
-        for (int t = 0; t < kTT; ++t) acc[b][t] = mfma32x32x16(wop[b], xc[t], acc[b][t]);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
+  };
+  if constexpr (DT == kBF16) k_loop(std::integral_constant<int, 0>{});
+  else if (f16_fast) k_loop(std::integral_constant<int, 1>{});
+  else k_loop(std::integral_constant<int, 2>{});
 
   // ---- epilogue --------------------------------------------------------
   // acc[b][t][v]: token tok0 + xtr[t], tile row block base + 8 (v/4) + 4 j + (v%4)
@@ -321,10 +375,10 @@ __global__ __launch_bounds__(NW * 64, 2) void gemm_ring_kernel(RingArgs a) {
           if constexpr (NMAT == 2) v[e] = silu_f32(acc[b][t][4 * g + e]) * acc[WB / 2 + b][t][4 * g + e];
           else v[e] = acc[b][t][4 * g + e];
         }
-        const uint32_t lo = (uint32_t)f32_to_act<kBF16>(v[0]) | ((uint32_t)f32_to_act<kBF16>(v[1]) << 16);
-        const uint32_t hi = (uint32_t)f32_to_act<kBF16>(v[2]) | ((uint32_t)f32_to_act<kBF16>(v[3]) << 16);
+        const uint32_t lo = (uint32_t)f32_to_act<DT>(v[0]) | ((uint32_t)f32_to_act<DT>(v[1]) << 16);
+        const uint32_t hi = (uint32_t)f32_to_act<DT>(v[2]) | ((uint32_t)f32_to_act<DT>(v[3]) << 16);
         const int64_t o = (int64_t)tok * N + orow;
-        *reinterpret_cast<u32x2_t*>(a.out + o) = with_residual4<kBF16>(u32x2_t{lo, hi}, a.res, o);
+        *reinterpret_cast<u32x2_t*>(a.out + o) = with_residual4<DT>(u32x2_t{lo, hi}, a.res, o);
       }
     }
   }
@@ -332,7 +386,7 @@ __global__ __launch_bounds__(NW * 64, 2) void gemm_ring_kernel(RingArgs a) {
 
 // out[m][n] = epilogue(sum over ks of ws[ks][m][n] (and [N + n] for up)), in
 // ks order; four outputs per thread.
-template <int NMAT>
+template <int NMAT, int DT>
 __global__ __launch_bounds__(256) void ring_reduce(const float* __restrict__ ws, uint16_t* out,
                                                    const uint16_t* res, int M, int N, int ksplit) {
   const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;   // group of 4 outputs
@@ -349,9 +403,9 @@ __global__ __launch_bounds__(256) void ring_reduce(const float* __restrict__ ws,
   float v[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) v[e] = NMAT == 2 ? silu_f32(g[e]) * u[e] : g[e];
-  const uint32_t lo = (uint32_t)f32_to_act<kBF16>(v[0]) | ((uint32_t)f32_to_act<kBF16>(v[1]) << 16);
-  const uint32_t hi = (uint32_t)f32_to_act<kBF16>(v[2]) | ((uint32_t)f32_to_act<kBF16>(v[3]) << 16);
-  *reinterpret_cast<u32x2_t*>(out + m * N + n) = with_residual4<kBF16>(u32x2_t{lo, hi}, res, m * N + n);
+  const uint32_t lo = (uint32_t)f32_to_act<DT>(v[0]) | ((uint32_t)f32_to_act<DT>(v[1]) << 16);
+  const uint32_t hi = (uint32_t)f32_to_act<DT>(v[2]) | ((uint32_t)f32_to_act<DT>(v[3]) << 16);
+  *reinterpret_cast<u32x2_t*>(out + m * N + n) = with_residual4<DT>(u32x2_t{lo, hi}, res, m * N + n);
 }
 
 // Number of K ranges per output tile.  Cost model (microseconds): a tile's
@@ -393,7 +447,7 @@ struct FixedWs {
   size_t bytes;
 };
 
-template <int NMAT, int BM, int WR, int NW = 8>
+template <int NMAT, int BM, int WR, int NW = 8, int DT = kBF16>
 hipError_t launch_ring(RingArgs r, hipStream_t st, FixedWs fixed) {
   using C = RingCfg<BM, NW>;
   constexpr int kRowsOut = NMAT == 2 ? 128 : 256;
@@ -420,18 +474,18 @@ hipError_t launch_ring(RingArgs r, hipStream_t st, FixedWs fixed) {
     kern<<<(unsigned)nwg, NW * 64, C::kLds, st>>>(r);
     return hipGetLastError();
   };
-  if (ksplit == 1) return go(gemm_ring_kernel<NMAT, BM, false, WR, NW>, tiles);
-  const hipError_t e = go(gemm_ring_kernel<NMAT, BM, true, WR, NW>, tiles * ksplit);
+  if (ksplit == 1) return go(gemm_ring_kernel<NMAT, BM, false, WR, NW, DT>, tiles);
+  const hipError_t e = go(gemm_ring_kernel<NMAT, BM, true, WR, NW, DT>, tiles * ksplit);
   if (e != hipSuccess) return e;
   const int64_t groups = (int64_t)r.M * r.N / 4;
-  ring_reduce<NMAT><<<(unsigned)((groups + 255) / 256), 256, 0, st>>>(r.ws, r.out, r.res, r.M, r.N, ksplit);
+  ring_reduce<NMAT, DT><<<(unsigned)((groups + 255) / 256), 256, 0, st>>>(r.ws, r.out, r.res, r.M, r.N, ksplit);
   return hipGetLastError();
 }
 
 }  // namespace
 
 bool gemm_ring_supported(const MlpArgs& a, int stage) {
-  if (option(kOptGemmRing) == 0 || a.dtype != kBF16) return false;
+  if (option(kOptGemmRing) == 0 || (a.dtype != kBF16 && a.dtype != kF16)) return false;
   if ((stage & kStageGateUp) && a.hidden % 512 != 0) return false;
   if ((stage & kStageDown) && a.inter % 512 != 0) return false;
   if (a.n > (1 << 24) || a.hidden > (1 << 20) || a.inter > (1 << 22)) return false;
@@ -456,7 +510,12 @@ hipError_t launch_gemm_ring_mlp(const MlpArgs& a, int stage, hipStream_t st) {
     const int wr = option(kOptRingWrGu);
     const int nw = option(kOptRingNwGu);
     hipError_t e;
-    if (nw == 4) e = wr == 2 ? launch_ring<2, 128, 2, 4>(r, st, fx) : launch_ring<2, 128, 4, 4>(r, st, fx);
+    if (a.dtype == kF16) {
+      // fp16: the default layout only (8 waves, 4 x 2)
+      if (a.n > 1024) e = launch_ring<2, 256, 4, 8, kF16>(r, st, fx);
+      else if (a.n <= kSmallTile) e = launch_ring<2, 64, 4, 8, kF16>(r, st, fx);
+      else e = launch_ring<2, 128, 4, 8, kF16>(r, st, fx);
+    } else if (nw == 4) e = wr == 2 ? launch_ring<2, 128, 2, 4>(r, st, fx) : launch_ring<2, 128, 4, 4>(r, st, fx);
     else if (a.n > 1024) e = wr == 2 ? launch_ring<2, 256, 2>(r, st, fx) : launch_ring<2, 256, 4>(r, st, fx);
     else if (a.n <= kSmallTile) e = launch_ring<2, 64, 4>(r, st, fx);
     else e = wr == 2 ? launch_ring<2, 128, 2>(r, st, fx) : launch_ring<2, 128, 4>(r, st, fx);
@@ -468,6 +527,8 @@ hipError_t launch_gemm_ring_mlp(const MlpArgs& a, int stage, hipStream_t st) {
                static_cast<const uint16_t*>(a.residual)};
     const int wr = option(kOptRingWrDn);
     const int nw = option(kOptRingNwDn);
+    if (a.dtype == kF16)
+      return a.n <= kSmallTile ? launch_ring<1, 64, 4, 8, kF16>(r, st, fx) : launch_ring<1, 128, 4, 8, kF16>(r, st, fx);
     if (nw == 4) return wr == 2 ? launch_ring<1, 64, 2, 4>(r, st, fx) : launch_ring<1, 64, 4, 4>(r, st, fx);
     if (a.n <= kSmallTile) return launch_ring<1, 64, 4>(r, st, fx);
     return wr == 2 ? launch_ring<1, 128, 2>(r, st, fx) : launch_ring<1, 128, 4>(r, st, fx);
