@@ -1,14 +1,15 @@
-"""GPU parity of the split-K tile kernels (9..64 bf16 tokens, K a multiple of
-1024): TI_PATH_SKINNY and TI_PATH_AUTO run them for small batches the decode
-kernels do not take.
+"""GPU parity of the split-K tile kernels (9..64 bf16 or fp16 tokens, K a
+multiple of 1024): TI_PATH_SKINNY and TI_PATH_AUTO run them for small batches
+the decode kernels do not take.
 
 Each stage is checked against the CPU oracle with the kernel's rounding
 points (exact fp32 sums, h rounded once), as for the decode kernels.  The
 cases cover one to four 16-token column tiles with a partial last one, one
 K range (Qwen3-0.6B gate_up) and 25 of them, a grid with fewer row groups
 than waves, scale bytes outside the hardware conversion's exact range (NaN
-included), the residual, and the dispatch (TINYINFER_TILE=0 switches the
-kernels off)."""
+included), fp16 activations (fp16 MFMAs, fp16-subnormal weights, and the
+exact hi + lo form for scale bytes below fp16's range), the residual, and the
+dispatch (TINYINFER_TILE=0 switches the kernels off)."""
 
 
 import numpy as np
@@ -138,6 +139,58 @@ def test_tile_gate_up_in_one_launch(capi, m, h, i):
         assert sum("tile_gu_kernel" in n for n in names["1"]) == 1, names["1"]
         assert not any("tile_reduce" in n for n in names["1"]), names["1"]
         assert sum("tile_reduce" in n for n in names["0"]) == 1, names["0"]
+
+
+@pytest.mark.parametrize("m", [9, 16, 33, 64])
+@pytest.mark.parametrize("h,i", [(4096, 12288), (1024, 3072), (1024, 25600)])
+def test_tile_fp16_stage_shapes(capi, m, h, i):
+    """fp16 activations on the tile kernels (fp16 MFMAs on weights converted to
+    fp16), at one to four column tiles and 1..25 K ranges."""
+    banner(f"tile fp16 stages m={m} h={h} i={i}")
+    x, mats = make_case(m, h, i, seed=31 * h + i + m, dtype=torch.float16)
+    stages(capi, x, mats, f"fp16 m={m} h={h} i={i}")
+
+
+@pytest.mark.parametrize("m", [16, 48])
+def test_tile_fp16_scale_paths(capi, m):
+    """fp16 with scale bytes 104..113 (fp16-subnormal weights, still the fp16
+    MFMA path) and below 104 (those row groups on exact bf16 weights against
+    the activations' bf16 hi and lo parts): every other output within the
+    bar, the rows that read only such a block exact to one fp16 unit."""
+    from tests.test_gpu_gemm import _isolate_block, _ulps_f16
+    from tests.test_gpu_stream import down_semantics
+    banner(f"tile fp16 scale paths m={m}")
+    x, mats = make_case(m, 1024, 2048, seed=97 + m, dtype=torch.float16)
+    gp, gs, up, us, dp, ds = [np.array(a) for a in mats]
+    gs[40, 3] = 90
+    us[1500, 20] = 95
+    rows = {5: 104, 333: 109, 600: 103, 1000: 113}
+    for row, byte in rows.items():
+        _isolate_block(dp, ds, [row], 7, byte)
+    mats = [gp, gs, up, us, dp, ds]
+    stages(capi, x, mats, "fp16 scale paths", cols=[c for c in range(1024) if c not in rows])
+    xd, md = to_dev(x, mats)
+    h_ref = h_semantics(x, gp, gs, up, us)
+    o = capi.down(h_ref.cuda(), md[4], md[5], path=SKINNY).cpu()
+    o_ref = down_semantics(h_ref, dp, ds)
+    for row in rows:
+        assert o_ref[:, row].float().abs().max() > 0
+        assert _ulps_f16(o[:, row], o_ref[:, row]) <= 1, row
+
+
+@pytest.mark.parametrize("m,h,i", [(16, 4096, 12288), (24, 2048, 6144)])
+def test_tile_fp16_gate_up_in_one_launch(capi, m, h, i):
+    """fp16 gate_up in one launch is bit-identical to the split kernel + reduce."""
+    banner(f"tile fp16 gate_up one launch m={m} h={h} i={i}")
+    x, mats = make_case(m, h, i, seed=950 + m + h, dtype=torch.float16)
+    xd, md = to_dev(x, mats)
+    out = {}
+    for flag in (1, 0):
+        with capi.option("TINYINFER_TILE_GU", flag):
+            out[flag] = capi.gate_up(xd, *md[:4], path=SKINNY)
+    torch.cuda.synchronize()
+    assert torch.equal(out[1].view(torch.int16), out[0].view(torch.int16))
+    check_close(out[1].cpu(), h_semantics(x, *mats[:4]), f"fp16 m={m} gate_up")
 
 
 @pytest.mark.parametrize("m", [16, 40])

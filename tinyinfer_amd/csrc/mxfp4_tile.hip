@@ -78,8 +78,12 @@ __device__ __forceinline__ uint32_t tile_scale(const TileBuf& b, int c) {
   return (b.s[c >> 2][c & 3] >> (8 * ((threadIdx.x >> 4) & 3))) & 0xffu;
 }
 
-// lds: the K range's activations, token t at lds + t * tstride
-template <int MT, bool FAST>
+// lds: the K range's activations, token t at lds + t * tstride.  MODE 0:
+// bf16 activations, hardware conversion; 1: bf16, exact conversion; 2: fp16
+// activations, weights converted to fp16 by the hardware (exact when every
+// scale byte is e8m0_f16_ok), fp16 MFMAs; 3: fp16 activations, exact bf16
+// weights against the activations' exact bf16 hi and lo parts (two MFMAs).
+template <int MT, int MODE>
 __device__ __forceinline__ void tile_mma(const TileBuf& b, const uint8_t* lds, int tstride, f32x4_t (&acc)[MT]) {
   const int lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
@@ -88,18 +92,40 @@ __device__ __forceinline__ void tile_mma(const TileBuf& b, const uint8_t* lds, i
     const uint32_t sb = tile_scale(b, c);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const u32x4_t wa = FAST ? dq8_bf16_fast(b.w[c][q], sb) : dq8_bf16_exact(b.w[c][q], sb);
+      const u32x4_t wa = MODE == 0   ? dq8_bf16_fast(b.w[c][q], sb)
+                         : MODE == 2 ? dq8_f16_fast(b.w[c][q], sb)
+                                     : dq8_bf16_exact(b.w[c][q], sb);
       const int ch = (4 * c + g) * 4 + q;   // 16-byte chunk of the range
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const u32x4_t xb = *reinterpret_cast<const u32x4_t*>(lds + (16 * mt + n) * tstride + 16 * (ch ^ n));
-        acc[mt] = mfma16x16x32(wa, xb, acc[mt]);
+        if constexpr (MODE == 2) {
+          acc[mt] = mfma16x16x32_f16(wa, xb, acc[mt]);
+        } else if constexpr (MODE == 3) {
+          u32x4_t xh, xl;
+          f16x8_split_bf16(xb, xh, xl);
+          acc[mt] = mfma16x16x32(wa, xl, mfma16x16x32(wa, xh, acc[mt]));
+        } else {
+          acc[mt] = mfma16x16x32(wa, xb, acc[mt]);
+        }
       }
     }
   }
 }
 
-template <int MT>
+// The group's multiply: per wave, the faster exact form its scale bytes allow.
+template <int MT, int DT>
+__device__ __forceinline__ void tile_group_mma(const TileBuf& b, const uint8_t* lds, int tstride,
+                                               f32x4_t (&acc)[MT]) {
+  bool ok = true;
+#pragma unroll
+  for (int c = 0; c < kRangeLoads; ++c)
+    ok = ok && (DT == kBF16 ? e8m0_fast_ok(tile_scale(b, c)) : e8m0_f16_ok(tile_scale(b, c)));
+  if (wave_all(ok)) tile_mma<MT, DT == kBF16 ? 0 : 2>(b, lds, tstride, acc);
+  else tile_mma<MT, DT == kBF16 ? 1 : 3>(b, lds, tstride, acc);
+}
+
+template <int MT, int DT>
 __global__ __launch_bounds__(kTThreads, 1) void tile_kernel(TileArgs a) {
   constexpr int kXPre = MT * 16 * (kRangeK / 8) / kTThreads;   // 16-byte x chunks per thread
   extern __shared__ __align__(16) uint8_t lds[];
@@ -138,16 +164,12 @@ __global__ __launch_bounds__(kTThreads, 1) void tile_kernel(TileArgs a) {
   asm volatile("" ::: "memory");
 
   const int nmr = a.nmat * a.R;
-  auto step = [&](TileBuf& b, int j, auto issue_tag) {
+  auto step = [&](TileBuf& b, int j, auto issue_tag) __attribute__((always_inline)) {
     const int G = group_of(j);
     f32x4_t acc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    bool ok = true;
-#pragma unroll
-    for (int c = 0; c < kRangeLoads; ++c) ok = ok && e8m0_fast_ok(tile_scale(b, c));
-    if (wave_all(ok)) tile_mma<MT, true>(b, lds, kTokenLds, acc);
-    else tile_mma<MT, false>(b, lds, kTokenLds, acc);
+    tile_group_mma<MT, DT>(b, lds, kTokenLds, acc);
     if constexpr (decltype(issue_tag)::value) tile_issue(a, group_of(j + 2), kr, b);
     // lane l holds rows 4 (l / 16) + v of the group, token 16 mt + l % 16
     const int rg = a.R / 16;
@@ -183,7 +205,7 @@ __global__ __launch_bounds__(kTThreads, 1) void tile_kernel(TileArgs a) {
 
 // out[m][n] = epilogue(sum over kr of ws[kr][m][n] (and [R + n] for up)), in
 // kr order; four outputs per thread.
-template <int NMAT>
+template <int NMAT, int DT>
 __global__ __launch_bounds__(256) void tile_reduce(const float* __restrict__ ws, uint16_t* out, const uint16_t* res,
                                                    int M, int mpad, int R, int nkr) {
   const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -216,9 +238,9 @@ __global__ __launch_bounds__(256) void tile_reduce(const float* __restrict__ ws,
   float v[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) v[e] = NMAT == 2 ? silu_f32(g[e]) * u[e] : g[e];
-  const uint32_t lo = (uint32_t)f32_to_act<kBF16>(v[0]) | ((uint32_t)f32_to_act<kBF16>(v[1]) << 16);
-  const uint32_t hi = (uint32_t)f32_to_act<kBF16>(v[2]) | ((uint32_t)f32_to_act<kBF16>(v[3]) << 16);
-  *reinterpret_cast<u32x2_t*>(out + m * R + n) = with_residual4<kBF16>(u32x2_t{lo, hi}, res, m * R + n);
+  const uint32_t lo = (uint32_t)f32_to_act<DT>(v[0]) | ((uint32_t)f32_to_act<DT>(v[1]) << 16);
+  const uint32_t hi = (uint32_t)f32_to_act<DT>(v[2]) | ((uint32_t)f32_to_act<DT>(v[3]) << 16);
+  *reinterpret_cast<u32x2_t*>(out + m * R + n) = with_residual4<DT>(u32x2_t{lo, hi}, res, m * R + n);
 }
 
 // gate_up without the K split, when all of x fits LDS (S = K / 1024 ranges,
@@ -229,7 +251,7 @@ __global__ __launch_bounds__(256) void tile_reduce(const float* __restrict__ ws,
 // in order, applies SiLU * up and stores h: no workspace round trip and no
 // reduce launch.  Every wave runs the same iterations (the barrier); blocks
 // past the end repeat the last one and store to `dummy` instead.
-template <int MT, int S>
+template <int MT, int S, int DT>
 __global__ __launch_bounds__(kTThreads, 1) void tile_gu_kernel(TileArgs a, uint16_t* out, uint16_t* dummy) {
   static_assert(S == 1 || S == 2 || S == 4, "8 waves = (4 / S) blocks x 2 matrices x S ranges");
   constexpr int kBlocks = 4 / S;
@@ -277,15 +299,11 @@ __global__ __launch_bounds__(kTThreads, 1) void tile_gu_kernel(TileArgs a, uint1
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 
-  auto step = [&](TileBuf& b, int it, auto issue_tag) {
+  auto step = [&](TileBuf& b, int it, auto issue_tag) __attribute__((always_inline)) {
     f32x4_t acc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    bool ok = true;
-#pragma unroll
-    for (int c = 0; c < kRangeLoads; ++c) ok = ok && e8m0_fast_ok(tile_scale(b, c));
-    if (wave_all(ok)) tile_mma<MT, true>(b, lds + sp * kTokenLds, tstride, acc);
-    else tile_mma<MT, false>(b, lds + sp * kTokenLds, tstride, acc);
+    tile_group_mma<MT, DT>(b, lds + sp * kTokenLds, tstride, acc);
     if constexpr (decltype(issue_tag)::value) tile_issue(a, mat * nrb + rb_of(it + 2), sp, b);
     float* pw = part + ((it & 1) * kTW + wave) * MT * 256;
 #pragma unroll
@@ -311,7 +329,7 @@ __global__ __launch_bounds__(kTThreads, 1) void tile_gu_kernel(TileArgs a, uint1
       const int rb = (it * (int)gridDim.x + (int)blockIdx.x) * kBlocks + bl;
       const bool valid = rb < nrb && t < a.M && (kOut >= kTThreads || (int)threadIdx.x < kOut);
       uint16_t* dst = valid ? out + (int64_t)t * a.R + rb * 16 + i : dummy + threadIdx.x;
-      *dst = f32_to_act<kBF16>(silu_f32(g) * u);
+      *dst = f32_to_act<DT>(silu_f32(g) * u);
     }
   };
   constexpr std::true_type kIssue{};
@@ -366,10 +384,10 @@ bool tile_plan(int64_t M, int64_t K, int64_t R, bool gateup, TileArgs& a, int& g
 
 bool aligned_tile(const void* p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) & (n - 1)) == 0; }
 
-template <int MT>
+template <int MT, int DT>
 hipError_t tile_launch(const TileArgs& a, int grid, hipStream_t st) {
   const int lds = MT * 16 * kTokenLds;
-  auto k = tile_kernel<MT>;
+  auto k = tile_kernel<MT, DT>;
   if (lds > 64 * 1024 &&
       hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, lds) !=
           hipSuccess)
@@ -387,10 +405,10 @@ bool tile_gu_fits(const TileArgs& a, int mt) {
 
 bool tile_gu_enabled() { return option(kOptTileGu) != 0; }
 
-template <int MT, int S>
+template <int MT, int S, int DT>
 hipError_t tile_gu_launch(const TileArgs& a, int grid, uint16_t* out, hipStream_t st) {
   const int lds = 16 * MT * S * kTokenLds + 2 * kTW * MT * 256 * (int)sizeof(float);
-  auto k = tile_gu_kernel<MT, S>;
+  auto k = tile_gu_kernel<MT, S, DT>;
   if (lds > 64 * 1024 &&
       hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, lds) !=
           hipSuccess)
@@ -400,14 +418,14 @@ hipError_t tile_gu_launch(const TileArgs& a, int grid, uint16_t* out, hipStream_
   return hipGetLastError();
 }
 
-template <bool GATEUP>
+template <bool GATEUP, int DT>
 hipError_t tile_stage(const MlpArgs& m, hipStream_t st) {
   TileArgs a;
   int grid = 0, mt = 0;
   size_t bytes = 0;
   const int64_t K = GATEUP ? m.hidden : m.inter;
   const int64_t R = GATEUP ? m.inter : m.hidden;
-  if (m.dtype != kBF16 || !tile_plan(m.n, K, R, GATEUP, a, grid, mt, bytes)) return hipErrorNotSupported;
+  if (m.dtype != DT || !tile_plan(m.n, K, R, GATEUP, a, grid, mt, bytes)) return hipErrorNotSupported;
   a.ws = m.ws ? (bytes <= m.ws_bytes ? m.ws : nullptr) : gemm_split_workspace(bytes, st);
   if (!a.ws) return hipErrorNotSupported;
   a.x = static_cast<const uint16_t*>(GATEUP ? m.x : m.tmp);
@@ -422,28 +440,28 @@ hipError_t tile_stage(const MlpArgs& m, hipStream_t st) {
       const int nrb = a.R / 16;
       const int g2 = std::min(tile_cus(), (nrb + kblocks - 1) / kblocks);
       switch (mt * 8 + S) {
-        case 8 + 1: return tile_gu_launch<1, 1>(a, g2, static_cast<uint16_t*>(m.tmp), st);
-        case 8 + 2: return tile_gu_launch<1, 2>(a, g2, static_cast<uint16_t*>(m.tmp), st);
-        case 8 + 4: return tile_gu_launch<1, 4>(a, g2, static_cast<uint16_t*>(m.tmp), st);
-        case 16 + 1: return tile_gu_launch<2, 1>(a, g2, static_cast<uint16_t*>(m.tmp), st);
-        case 16 + 2: return tile_gu_launch<2, 2>(a, g2, static_cast<uint16_t*>(m.tmp), st);
+        case 8 + 1: return tile_gu_launch<1, 1, DT>(a, g2, static_cast<uint16_t*>(m.tmp), st);
+        case 8 + 2: return tile_gu_launch<1, 2, DT>(a, g2, static_cast<uint16_t*>(m.tmp), st);
+        case 8 + 4: return tile_gu_launch<1, 4, DT>(a, g2, static_cast<uint16_t*>(m.tmp), st);
+        case 16 + 1: return tile_gu_launch<2, 1, DT>(a, g2, static_cast<uint16_t*>(m.tmp), st);
+        case 16 + 2: return tile_gu_launch<2, 2, DT>(a, g2, static_cast<uint16_t*>(m.tmp), st);
         default: break;
       }
     }
   }
   hipError_t e = hipErrorNotSupported;
   switch (mt) {
-    case 1: e = tile_launch<1>(a, grid, st); break;
-    case 2: e = tile_launch<2>(a, grid, st); break;
-    case 3: e = tile_launch<3>(a, grid, st); break;
-    case 4: e = tile_launch<4>(a, grid, st); break;
+    case 1: e = tile_launch<1, DT>(a, grid, st); break;
+    case 2: e = tile_launch<2, DT>(a, grid, st); break;
+    case 3: e = tile_launch<3, DT>(a, grid, st); break;
+    case 4: e = tile_launch<4, DT>(a, grid, st); break;
     default: break;
   }
   if (e != hipSuccess) return e;
   uint16_t* out = static_cast<uint16_t*>(GATEUP ? m.tmp : m.out);
   const uint16_t* res = GATEUP ? nullptr : static_cast<const uint16_t*>(m.residual);
   const int64_t groups = m.n * R / 4;
-  tile_reduce<GATEUP ? 2 : 1><<<(unsigned)((groups + 255) / 256), 256, 0, st>>>(a.ws, out, res, a.M, a.mpad, a.R,
+  tile_reduce<GATEUP ? 2 : 1, DT><<<(unsigned)((groups + 255) / 256), 256, 0, st>>>(a.ws, out, res, a.M, a.mpad, a.R,
                                                                                  a.nkr);
   return hipGetLastError();
 }
@@ -453,7 +471,7 @@ hipError_t tile_stage(const MlpArgs& m, hipStream_t st) {
 bool tile_enabled() { return option(kOptTile) != 0; }
 
 size_t tile_workspace_need(const MlpArgs& m, int stage) {
-  if (m.dtype != kBF16) return 0;
+  if (m.dtype != kBF16 && m.dtype != kF16) return 0;
   if ((stage & kStageGateUp) && m.norm_w != nullptr) return 0;
   TileArgs a;
   int grid = 0, mt = 0;
@@ -484,11 +502,12 @@ bool tile_supported(const MlpArgs& m, int stage, hipStream_t st) {
 }
 
 hipError_t launch_tile_mlp(const MlpArgs& m, int stage, hipStream_t st) {
+  const bool f16 = m.dtype == kF16;
   if (stage & kStageGateUp) {
-    const hipError_t e = tile_stage<true>(m, st);
+    const hipError_t e = f16 ? tile_stage<true, kF16>(m, st) : tile_stage<true, kBF16>(m, st);
     if (e != hipSuccess) return e;
   }
-  if (stage & kStageDown) return tile_stage<false>(m, st);
+  if (stage & kStageDown) return f16 ? tile_stage<false, kF16>(m, st) : tile_stage<false, kBF16>(m, st);
   return hipSuccess;
 }
 
