@@ -1,14 +1,17 @@
 """GPU parity of the row-streaming kernels (one token, one launch per MLP
 stage): TI_PATH_SKINNY and TI_PATH_AUTO run them for N == 1 when K % 128 == 0
-and the stage's K fits (gate_up K <= 8192, down K <= 12288, fp16 K <= 6144).
+and the stage's K fits the chunk limits (a wave holds at most 4 chunks of 2048
+K elements for gate_up, 6 for down; with fp16 activations 2 and 3; a row is
+shared by at most 2 waves for gate_up, 4 for down).
 
 Each stage is checked against the CPU oracle with the kernel's rounding
 points (exact sums, h rounded once), as for the 8-row stream kernels.  The
 shapes cover the kernel's edge cases: a last chunk with fewer than 64 blocks
 (K not a multiple of 2048), waves with no row and waves with many, every
 instantiated chunk count, scale bytes outside the hardware conversion's exact
-range (NaN included), fp16 activations, the residual and the RMSNorm
-prologue.  TINYINFER_ROWSTREAM=0 switches the library back to the 8-row
+range (NaN included), fp16 activations (fp16 MFMAs; fp16-subnormal weights;
+the exact hi + lo form for scale bytes below fp16's range), the residual and
+the RMSNorm prologue.  TINYINFER_ROWSTREAM=0 switches the library back to the 8-row
 stream kernels for N == 1, which the last tests compare against."""
 
 
@@ -95,11 +98,37 @@ def test_rowstream_scale_bytes_outside_fast_range(capi):
     assert torch.isnan(y[0, 1500]) and torch.isfinite(y[0, rest]).all()
 
 
-@pytest.mark.parametrize("h,i", [(1024, 3072), (2560, 6144), (6144, 2048), (1024, 8192)])
+@pytest.mark.parametrize("h,i", [(1024, 3072), (2560, 6144), (6144, 2048), (1024, 8192), (4096, 12288),
+                                 (8192, 6144), (2048, 24576)])
 def test_rowstream_fp16(capi, h, i):
     banner(f"rowstream fp16 h={h} i={i}")
     x, mats = make_case(1, h, i, seed=31 + h, dtype=torch.float16)
     stages(capi, x, mats, f"fp16 h={h} i={i}")
+
+
+def test_rowstream_fp16_scale_paths(capi):
+    """fp16 with scale bytes 104..113 (fp16-subnormal weights, fp16 MFMAs)
+    and below 104 (those rows on exact bf16 weights against x's bf16 hi and
+    lo parts): every other output within the bar, the rows that read only
+    such a block exact to one fp16 unit."""
+    from tests.test_gpu_gemm import _isolate_block, _ulps_f16
+    banner("rowstream fp16 scale paths")
+    x, mats = make_case(1, 2048, 6144, seed=77, dtype=torch.float16)
+    gp, gs, up, us, dp, ds = [np.array(a) for a in mats]
+    gs[40, 3] = 90
+    us[1500, 20] = 95
+    rows = {5: 104, 333: 109, 600: 103, 1000: 113}
+    for row, byte in rows.items():
+        _isolate_block(dp, ds, [row], 7, byte)
+    mats = [gp, gs, up, us, dp, ds]
+    stages(capi, x, mats, "fp16 scale paths", cols=[c for c in range(2048) if c not in rows])
+    xd, md = to_dev(x, mats)
+    h_ref = h_semantics(x, gp, gs, up, us)
+    o = capi.down(h_ref.cuda(), md[4], md[5], path=SKINNY).cpu()
+    o_ref = down_semantics(h_ref, dp, ds)
+    for row in rows:
+        assert o_ref[:, row].float().abs().max() > 0
+        assert _ulps_f16(o[:, row], o_ref[:, row]) <= 1, row
 
 
 def test_rowstream_residual_and_full_call(capi):

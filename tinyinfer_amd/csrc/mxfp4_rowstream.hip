@@ -42,7 +42,7 @@ constexpr int kRW = 8;                 // waves per workgroup
 constexpr int kRThreads = kRW * 64;
 constexpr int kChunkBlocks = 64;       // 32-element blocks per load (1 KB of fp4)
 constexpr int kChunkK = kChunkBlocks * kBlock;
-constexpr int kMaxUC = 6;              // chunks per wave (down; gate_up 4, fp16 3)
+constexpr int kMaxUC = 6;              // chunks per wave (down; gate_up 4)
 
 struct RowArgs {
   const uint16_t* x;       // [K] activations (x for gate_up, h for down)
@@ -119,8 +119,11 @@ __device__ __forceinline__ uint32_t scale_byte(uint32_t dw) {
 // otherwise what a wave spends its time on once its rows have landed).  FULL: every lane of
 // every slot holds a real block; otherwise slots past the range (they hold a
 // repeat of its last chunk) and lanes past K multiply a zero
-// weight (scale 1.0) by the zero activation they hold.  FAST: every scale
-// byte in the hardware conversion's exact range.
+// weight (scale 1.0) by the zero activation they hold.  bf16: FAST when
+// every scale byte is in the hardware bf16 conversion's exact range.  fp16
+// (x held as fp16): FAST when every scale byte is e8m0_f16_ok, the weights
+// converted to fp16 on fp16 MFMAs; otherwise the exact bf16 weights against
+// x's exact bf16 hi and lo parts, two MFMAs.
 template <int DT, int UC, bool GATEUP, bool FAST, bool FULL, int T>
 __device__ __forceinline__ void mma_row(const RowArgs& a, int cb, int ncs, const RowBuf<UC, GATEUP>& b,
                                         const u32x4_t (&xr)[T][UC][4], const u32x4_t (&xl)[T][UC][4],
@@ -137,31 +140,23 @@ __device__ __forceinline__ void mma_row(const RowArgs& a, int cb, int ncs, const
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const uint32_t wq = valid ? b.w[m * UC + q][t] : 0u;
-        const u32x4_t wa = FAST ? dq8_bf16_fast(wq, sb) : dq8_bf16_exact(wq, sb);
+        const u32x4_t wa = !FAST ? dq8_bf16_exact(wq, sb) : DT == kBF16 ? dq8_bf16_fast(wq, sb) : dq8_f16_fast(wq, sb);
 #pragma unroll
         for (int tk = 0; tk < T; ++tk) {
           f32x4_t& c = acc[m][tk][t % kCh];
           if constexpr (DT == kBF16) {
             c = mfma16x16x32(wa, xr[tk][q][t], c);
+          } else if constexpr (FAST) {
+            c = mfma16x16x32_f16(wa, xr[tk][q][t], c);
           } else {
-            c = mfma16x16x32(wa, xl[tk][q][t], mfma16x16x32(wa, xr[tk][q][t], c));
+            u32x4_t xh, xlo;
+            f16x8_split_bf16(xr[tk][q][t], xh, xlo);
+            c = mfma16x16x32(wa, xlo, mfma16x16x32(wa, xh, c));
           }
         }
       }
     }
   }
-}
-
-// fp16 x8 from its exact bf16 hi + lo split (inverse of f16x8_split_bf16).
-__device__ __forceinline__ u32x4_t join_f16x8(const u32x4_t& hi, const u32x4_t& lo) {
-  u32x4_t o;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float a0 = __uint_as_float(hi[j] << 16) + __uint_as_float(lo[j] << 16);
-    const float a1 = __uint_as_float(hi[j] & 0xffff0000u) + __uint_as_float(lo[j] & 0xffff0000u);
-    o[j] = (uint32_t)f32_to_f16_rne(a0) | ((uint32_t)f32_to_f16_rne(a1) << 16);
-  }
-  return o;
 }
 
 // Sum of the diagonal of a 16x16 accumulator (lane l holds C[4(l/16)+v][l%16]).
@@ -287,8 +282,7 @@ __global__ __launch_bounds__(kRThreads, 1) void rowstream_kernel(RowArgs a) {
   }
 
   // lane l's activations: block 64c + l of each of its chunks c = cb + q,
-  // zero past K; with a norm, x <- round(w * x * inv).  fp16 is split into
-  // exact bf16 hi + lo.
+  // zero past K; with a norm, x <- round(w * x * inv).
   u32x4_t xr[T][UC][4], xl[T][UC][4];
 #pragma unroll
   for (int tk = 0; tk < T; ++tk) {
@@ -311,12 +305,8 @@ __global__ __launch_bounds__(kRThreads, 1) void rowstream_kernel(RowArgs a) {
           }
         }
         if (!valid) v = u32x4_t{0u, 0u, 0u, 0u};
-        if constexpr (DT == kBF16) {
-          xr[tk][q][t] = v;
-          xl[tk][q][t] = v;
-        } else {
-          f16x8_split_bf16(v, xr[tk][q][t], xl[tk][q][t]);
-        }
+        xr[tk][q][t] = v;
+        xl[tk][q][t] = v;
       }
     }
   }
@@ -333,7 +323,8 @@ __global__ __launch_bounds__(kRThreads, 1) void rowstream_kernel(RowArgs a) {
         for (int c = 0; c < kCh; ++c) acc[m][tk][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     bool ok = true;
 #pragma unroll
-    for (int k = 0; k < RowBuf<UC, GATEUP>::kMats * UC; ++k) ok = ok && e8m0_fast_ok(scale_byte(b.s[k]));
+    for (int k = 0; k < RowBuf<UC, GATEUP>::kMats * UC; ++k)
+      ok = ok && (DT == kBF16 ? e8m0_fast_ok(scale_byte(b.s[k])) : e8m0_f16_ok(scale_byte(b.s[k])));
     if (wave_all(ok)) {
       if (a.full && ncs == UC) mma_row<DT, UC, GATEUP, true, true, T>(a, cb, ncs, b, xr, xl, acc);
       else mma_row<DT, UC, GATEUP, true, false, T>(a, cb, ncs, b, xr, xl, acc);
@@ -410,8 +401,7 @@ __global__ __launch_bounds__(kRThreads, 1) void rowstream_kernel(RowArgs a) {
         if (q < ncs && blk < a.nblk) {
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
-            u32x4_t v = xr[tk][q][t];
-            if constexpr (DT != kBF16) v = join_f16x8(xr[tk][q][t], xl[tk][q][t]);
+            const u32x4_t v = xr[tk][q][t];
             *reinterpret_cast<u32x4_t*>(a.xn + (int64_t)tk * a.K + 32 * blk + 8 * t) = v;
           }
         }
@@ -427,7 +417,8 @@ bool aligned16_ptr(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u
 
 // Waves per row S and chunks per wave UC for a stage: S in {1, 2, 4} (gate_up
 // 1, 2) so that the largest share fits the VGPR budget (gate_up 4 chunks: two
-// matrices in flight; down 6; fp16 3, its activations are held as hi + lo)
+// matrices in flight; down 6; fp16 2 and 3, whose kernels also hold the
+// exact hi + lo form)
 // and, for down, holds at most 3 chunks where possible; or the S that
 // TINYINFER_ROW_SPLIT_GATEUP / _DOWN names, if that fits.
 bool row_plan(int64_t M, int64_t K, int64_t R, bool gateup, bool norm, int dtype, RowArgs& a, int& grid,
@@ -442,7 +433,7 @@ bool row_plan(int64_t M, int64_t K, int64_t R, bool gateup, bool norm, int dtype
   if (M == 2 && gateup) return false;
   const int nc = (int)((K + kChunkK - 1) / kChunkK);
   // chunks per wave: activations of every chunk and token stay in VGPRs
-  const int ucmax = dtype != kBF16 ? 3 : M == 2 ? (gateup ? 2 : 3) : gateup ? 4 : kMaxUC;
+  const int ucmax = dtype != kBF16 ? (gateup ? 2 : 3) : M == 2 ? (gateup ? 2 : 3) : gateup ? 4 : kMaxUC;
   const int smax = gateup ? 2 : 4;
   S = 0;
   const int want = option(gateup ? kOptRowSplitGateUp : kOptRowSplitDown);
@@ -489,10 +480,11 @@ hipError_t row_launch(const RowArgs& a, int grid, int64_t lds, hipStream_t st) {
 }
 
 // The instantiated (UC, S, T): one token: gate_up S = 1, 2 with UC <= 4, down
-// S = 1, 2, 4 with UC <= 6 (fp16 UC <= 3); two tokens (bf16): down UC <= 3.
+// S = 1, 2, 4 with UC <= 6 (fp16: gate_up UC <= 2, down UC <= 3); two tokens
+// (bf16): down UC <= 3.
 template <int DT, bool GATEUP, int S, int T>
 hipError_t row_dispatch_s(const RowArgs& a, int uc, int grid, int64_t lds, hipStream_t st) {
-  constexpr int kMax = DT != kBF16 ? 3 : T == 2 ? (GATEUP ? 2 : 3) : GATEUP ? 4 : kMaxUC;
+  constexpr int kMax = DT != kBF16 ? (GATEUP ? 2 : 3) : T == 2 ? (GATEUP ? 2 : 3) : GATEUP ? 4 : kMaxUC;
   switch (uc) {
     case 1: if constexpr (S == 1 || GATEUP) return row_launch<DT, 1, GATEUP, S, T>(a, grid, lds, st); break;
     case 2: return row_launch<DT, 2, GATEUP, S, T>(a, grid, lds, st);
