@@ -1,5 +1,5 @@
-"""GPU parity of the row-pair kernels (2..4 bf16 tokens, one launch per MLP
-stage): TI_PATH_SKINNY and TI_PATH_AUTO run them for 2 <= N <= 4 when K % 128
+"""GPU parity of the row-pair kernels (2..4 bf16 or fp16 tokens, one launch
+per MLP stage): TI_PATH_SKINNY and TI_PATH_AUTO run them for 2 <= N <= 4 when K % 128
 == 0 and a wave's share of a row pair fits its registers.
 
 Each stage is checked against the CPU oracle with the kernel's rounding
@@ -8,7 +8,8 @@ shapes cover the kernel's edge cases: a last chunk with fewer than 32 blocks
 (K not a multiple of 1024), waves with no pair and waves with many, one to
 four waves per pair, an odd token count (the second MFMA pass half empty),
 scale bytes outside the hardware conversion's exact range (NaN included),
-the residual and the RMSNorm prologue.  TINYINFER_ROWPAIR=0 switches the
+fp16 activations (fp16 MFMAs, fp16-subnormal weights, the exact hi + lo form
+below fp16's range), the residual and the RMSNorm prologue.  TINYINFER_ROWPAIR=0 switches the
 library back to the row / 8-row stream kernels, which the last tests compare
 against."""
 
@@ -48,6 +49,62 @@ def test_rowpair_stage_shapes(capi, m, h, i):
     banner(f"rowpair stages m={m} h={h} i={i}")
     x, mats = make_case(m, h, i, seed=13 * h + i + m)
     stages(capi, x, mats, f"m={m} h={h} i={i}")
+
+
+@pytest.mark.parametrize("m", [2, 3, 4])
+@pytest.mark.parametrize("h,i", [(4096, 12288), (1152, 5120), (1024, 3072), (3072, 128)])
+def test_rowpair_fp16_stage_shapes(capi, m, h, i):
+    """fp16 activations (fewer chunks per wave than bf16: stages beyond them
+    run on the other decode kernels, also checked here)."""
+    banner(f"rowpair fp16 stages m={m} h={h} i={i}")
+    x, mats = make_case(m, h, i, seed=19 * h + i + m, dtype=torch.float16)
+    stages(capi, x, mats, f"fp16 m={m} h={h} i={i}")
+
+
+def test_rowpair_fp16_runs_here_and_scale_paths(capi):
+    """At two fp16 tokens the down stage of a 2048 x 6144 MLP runs on the
+    row-pair kernels; scale bytes 104..113 (fp16-subnormal weights) and
+    below 104 (exact hi + lo form): every other output within the bar, the
+    rows that read only such a block exact to one fp16 unit."""
+    from tests.test_gpu_gemm import _isolate_block, _ulps_f16
+    from tests.test_gpu_stream import down_semantics
+    banner("rowpair fp16 scale paths")
+    x, mats = make_case(2, 2048, 6144, seed=78, dtype=torch.float16)
+    gp, gs, up, us, dp, ds = [np.array(a) for a in mats]
+    gs[40, 3] = 90
+    us[1500, 20] = 95
+    rows = {5: 104, 333: 109, 600: 103, 1000: 113}
+    for row, byte in rows.items():
+        _isolate_block(dp, ds, [row], 7, byte)
+    mats = [gp, gs, up, us, dp, ds]
+    stages(capi, x, mats, "fp16 scale paths", cols=[c for c in range(2048) if c not in rows])
+    xd, md = to_dev(x, mats)
+    h_ref = h_semantics(x, gp, gs, up, us)
+    names = kernel_names(lambda: capi.down(h_ref.cuda(), md[4], md[5], path=SKINNY))
+    o = capi.down(h_ref.cuda(), md[4], md[5], path=SKINNY).cpu()
+    o_ref = down_semantics(h_ref, dp, ds)
+    for row in rows:
+        assert o_ref[:, row].float().abs().max() > 0
+        assert _ulps_f16(o[:, row], o_ref[:, row]) <= 1, row
+    if names:
+        assert any("rowpair_kernel" in n for n in names), names
+
+
+def test_rowpair_fp16_norm_residual(capi):
+    """The fused layer half in fp16 at two tokens: xn within one fp16 rounding
+    of the oracle's norm, the output bit-identical to the unfused composition."""
+    banner("rowpair fp16 norm + residual")
+    x, mats = make_case(2, 4096, 12288, seed=71, dtype=torch.float16)
+    xd, md = to_dev(x, mats)
+    w = (torch.rand(4096, generator=torch.Generator().manual_seed(3)) + 0.5).to(torch.float16)
+    out, xn = capi.mlp_forward_rmsnorm(xd, w.cuda(), 1e-6, *md, path=SKINNY)
+    plain = capi.mlp_forward(xn, *md, path=SKINNY, residual=xd)
+    torch.cuda.synchronize()
+    xn_ref = om.rmsnorm_reference(x, w, 1e-6)
+    rel = ((xn.cpu().float() - xn_ref.float()).abs() / xn_ref.float().abs().clamp_min(1e-30)).max()
+    assert float(rel) <= 2 ** -10, f"xn max rel {float(rel)}"
+    assert torch.equal(out.view(torch.int16), plain.view(torch.int16))
+    assert_parity(out.cpu(), om.decoder_mlp_reference(x, w, 1e-6, *mats), "fp16 norm + mlp")
 
 
 def test_rowpair_falls_back_beyond_its_registers(capi):

@@ -104,8 +104,12 @@ __device__ __forceinline__ void issue_pair(const PairArgs& a, int64_t pr, int cb
 }
 
 // P passes (tokens 2p + (lane & 1)) over each dequantized operand; 4 / P
-// accumulator chains per (matrix, pass).
-template <int UC, bool GATEUP, bool FAST, bool FULL, int P>
+// accumulator chains per (matrix, pass).  bf16: FAST when every scale byte is
+// in the hardware bf16 conversion's exact range.  fp16 (x held as fp16): FAST
+// when every scale byte is e8m0_f16_ok, the weights converted to fp16 on
+// fp16 MFMAs; otherwise the exact bf16 weights against x's exact bf16 hi and
+// lo parts, two MFMAs.
+template <int UC, bool GATEUP, bool FAST, bool FULL, int P, int DT>
 __device__ __forceinline__ void mma_pair(const PairArgs& a, int cb, int ncs, const PairBuf<UC, GATEUP>& b,
                                          const u32x4_t (&xr)[P][UC][4], f32x4_t (&acc)[2][P][4 / P]) {
   constexpr int kMats = GATEUP ? 2 : 1;
@@ -120,9 +124,20 @@ __device__ __forceinline__ void mma_pair(const PairArgs& a, int cb, int ncs, con
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const uint32_t wq = valid ? b.w[m * UC + q][t] : 0u;
-        const u32x4_t wa = FAST ? dq8_bf16_fast(wq, sb) : dq8_bf16_exact(wq, sb);
+        const u32x4_t wa = !FAST ? dq8_bf16_exact(wq, sb) : DT == kBF16 ? dq8_bf16_fast(wq, sb) : dq8_f16_fast(wq, sb);
 #pragma unroll
-        for (int p = 0; p < P; ++p) acc[m][p][t % kCh] = mfma16x16x32(wa, xr[p][q][t], acc[m][p][t % kCh]);
+        for (int p = 0; p < P; ++p) {
+          f32x4_t& c = acc[m][p][t % kCh];
+          if constexpr (DT == kBF16) {
+            c = mfma16x16x32(wa, xr[p][q][t], c);
+          } else if constexpr (FAST) {
+            c = mfma16x16x32_f16(wa, xr[p][q][t], c);
+          } else {
+            u32x4_t xh, xl;
+            f16x8_split_bf16(xr[p][q][t], xh, xl);
+            c = mfma16x16x32(wa, xl, mfma16x16x32(wa, xh, c));
+          }
+        }
       }
     }
   }
@@ -149,7 +164,7 @@ __device__ __forceinline__ void pair_partials(const f32x4_t& c, float* blk) {
   }
 }
 
-template <int UC, bool GATEUP, int S, int P>
+template <int UC, bool GATEUP, int S, int P, int DT>
 __global__ __launch_bounds__(kPThreads, 1) void rowpair_kernel(PairArgs a) {
   static_assert(kPW % S == 0, "the waves sharing a pair are in one workgroup");
   constexpr int kT = 2 * P;                // token slots
@@ -211,8 +226,8 @@ __global__ __launch_bounds__(kPThreads, 1) void rowpair_kernel(PairArgs a) {
         float s2 = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const float lo = act_to_f32<kBF16>((uint16_t)(xv[p][j] & 0xffffu));
-          const float hi = act_to_f32<kBF16>((uint16_t)(xv[p][j] >> 16));
+          const float lo = act_to_f32<DT>((uint16_t)(xv[p][j] & 0xffffu));
+          const float hi = act_to_f32<DT>((uint16_t)(xv[p][j] >> 16));
           s2 += lo * lo;
           s2 += hi * hi;
         }
@@ -269,9 +284,9 @@ __global__ __launch_bounds__(kPThreads, 1) void rowpair_kernel(PairArgs a) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const float lo =
-                act_to_f32<kBF16>((uint16_t)(g[j] & 0xffffu)) * act_to_f32<kBF16>((uint16_t)(v[j] & 0xffffu)) * iv;
-            const float hi = act_to_f32<kBF16>((uint16_t)(g[j] >> 16)) * act_to_f32<kBF16>((uint16_t)(v[j] >> 16)) * iv;
-            v[j] = (uint32_t)f32_to_act<kBF16>(lo) | ((uint32_t)f32_to_act<kBF16>(hi) << 16);
+                act_to_f32<DT>((uint16_t)(g[j] & 0xffffu)) * act_to_f32<DT>((uint16_t)(v[j] & 0xffffu)) * iv;
+            const float hi = act_to_f32<DT>((uint16_t)(g[j] >> 16)) * act_to_f32<DT>((uint16_t)(v[j] >> 16)) * iv;
+            v[j] = (uint32_t)f32_to_act<DT>(lo) | ((uint32_t)f32_to_act<DT>(hi) << 16);
           }
         }
         xr[p][q][t] = valid ? v : u32x4_t{0u, 0u, 0u, 0u};
@@ -290,12 +305,13 @@ __global__ __launch_bounds__(kPThreads, 1) void rowpair_kernel(PairArgs a) {
         for (int c = 0; c < kCh; ++c) acc[m][p][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     bool ok = true;
 #pragma unroll
-    for (int k = 0; k < PairBuf<UC, GATEUP>::kMats * UC; ++k) ok = ok && e8m0_fast_ok(pair_scale_byte(b.s[k]));
+    for (int k = 0; k < PairBuf<UC, GATEUP>::kMats * UC; ++k)
+      ok = ok && (DT == kBF16 ? e8m0_fast_ok(pair_scale_byte(b.s[k])) : e8m0_f16_ok(pair_scale_byte(b.s[k])));
     if (wave_all(ok)) {
-      if (a.full && ncs == UC) mma_pair<UC, GATEUP, true, true, P>(a, cb, ncs, b, xr, acc);
-      else mma_pair<UC, GATEUP, true, false, P>(a, cb, ncs, b, xr, acc);
+      if (a.full && ncs == UC) mma_pair<UC, GATEUP, true, true, P, DT>(a, cb, ncs, b, xr, acc);
+      else mma_pair<UC, GATEUP, true, false, P, DT>(a, cb, ncs, b, xr, acc);
     } else {
-      mma_pair<UC, GATEUP, false, false, P>(a, cb, ncs, b, xr, acc);
+      mma_pair<UC, GATEUP, false, false, P, DT>(a, cb, ncs, b, xr, acc);
     }
     if constexpr (decltype(issue_tag)::value) issue_pair<UC, GATEUP>(a, pair_of(j + 2), cb, ncs, b);
 #pragma unroll
@@ -352,7 +368,7 @@ __global__ __launch_bounds__(kPThreads, 1) void rowpair_kernel(PairArgs a) {
       }
       const float v = GATEUP ? silu_f32(y0) * y1 : y0;
       const int64_t idx = (int64_t)tk * a.R + 2 * pr + r;
-      a.out[idx] = with_residual<kBF16>(f32_to_act<kBF16>(v), a.res, idx);
+      a.out[idx] = with_residual<DT>(f32_to_act<DT>(v), a.res, idx);
     }
   }
   if (norm && blockIdx.x == 0 && wave < S && a.xn) {
@@ -378,16 +394,18 @@ int pair_cus() { return device_info().cus; }
 // chunks fit (4 at one pass, 3 at two), down at most 3 chunks per wave where
 // four waves suffice; more waves per pair when there are too few pairs to
 // give every CU a workgroup.
-bool pair_plan(int64_t M, int64_t K, int64_t R, bool gateup, bool norm, PairArgs& a, int& grid, int64_t& lds,
-               int& S, int& uc) {
+bool pair_plan(int64_t M, int64_t K, int64_t R, bool gateup, bool norm, int dtype, PairArgs& a, int& grid,
+               int64_t& lds, int& S, int& uc) {
   const int cus = pair_cus();
   if (cus < 1 || M < 2 || M > 4 || K < 128 || K % 128 != 0 || K > (1 << 20) || R < 2 || R % 2 != 0 ||
       R > (1 << 24))
     return false;
   const int P = (int)((M + 1) / 2);
   const int nc = (int)((K + kPairChunkK - 1) / kPairChunkK);
-  const int ucmax = gateup ? (P == 1 ? 4 : 3) : (P == 1 ? 6 : 4);
-  const int ucpref = gateup ? ucmax : 3;
+  // fp16 kernels also hold the exact hi + lo form: fewer chunks per wave
+  const int ucmax = dtype != kBF16 ? (gateup ? (P == 1 ? 2 : 1) : (P == 1 ? 3 : 2))
+                                   : gateup ? (P == 1 ? 4 : 3) : (P == 1 ? 6 : 4);
+  const int ucpref = gateup ? ucmax : std::min(3, ucmax);
   S = 0;
   for (int s = 1; S == 0 && s <= 4; s *= 2)
     if ((nc + s - 1) / s <= ucpref && s <= nc) S = s;
@@ -401,6 +419,7 @@ bool pair_plan(int64_t M, int64_t K, int64_t R, bool gateup, bool norm, PairArgs
   // too few pairs to give every CU a workgroup: more waves per pair
   while (S < 4 && 2 * S <= nc && (npairs * S + kPW - 1) / kPW < cus) S *= 2;
   uc = (nc + S - 1) / S;
+  if (uc > ucmax) return false;              // no kernel instantiated for it
   grid = (int)std::min<int64_t>(cus, (npairs * S + kPW - 1) / kPW);
   const int64_t nslots = (int64_t)grid * (kPW / S);
   a.M = (int)M;
@@ -422,9 +441,9 @@ bool pair_plan(int64_t M, int64_t K, int64_t R, bool gateup, bool norm, PairArgs
   return lds <= 160 * 1024;
 }
 
-template <int UC, bool GATEUP, int S, int P>
+template <int UC, bool GATEUP, int S, int P, int DT>
 hipError_t pair_launch(const PairArgs& a, int grid, int64_t lds, hipStream_t st) {
-  auto k = rowpair_kernel<UC, GATEUP, S, P>;
+  auto k = rowpair_kernel<UC, GATEUP, S, P, DT>;
   if (lds > 64 * 1024 &&
       hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
           hipSuccess)
@@ -433,26 +452,27 @@ hipError_t pair_launch(const PairArgs& a, int grid, int64_t lds, hipStream_t st)
   return hipGetLastError();
 }
 
-template <bool GATEUP, int S, int P>
+template <bool GATEUP, int S, int P, int DT>
 hipError_t pair_dispatch_s(const PairArgs& a, int uc, int grid, int64_t lds, hipStream_t st) {
-  constexpr int kMax = GATEUP ? (P == 1 ? 4 : 3) : (P == 1 ? 6 : 4);
+  constexpr int kMax = DT != kBF16 ? (GATEUP ? (P == 1 ? 2 : 1) : (P == 1 ? 3 : 2))
+                                   : GATEUP ? (P == 1 ? 4 : 3) : (P == 1 ? 6 : 4);
   switch (uc) {
-    case 1: return pair_launch<1, GATEUP, S, P>(a, grid, lds, st);
-    case 2: return pair_launch<2, GATEUP, S, P>(a, grid, lds, st);
-    case 3: return pair_launch<3, GATEUP, S, P>(a, grid, lds, st);
-    case 4: if constexpr (kMax >= 4) return pair_launch<4, GATEUP, S, P>(a, grid, lds, st); break;
-    case 5: if constexpr (kMax >= 5) return pair_launch<5, GATEUP, S, P>(a, grid, lds, st); break;
-    case 6: if constexpr (kMax >= 6) return pair_launch<6, GATEUP, S, P>(a, grid, lds, st); break;
+    case 1: return pair_launch<1, GATEUP, S, P, DT>(a, grid, lds, st);
+    case 2: if constexpr (kMax >= 2) return pair_launch<2, GATEUP, S, P, DT>(a, grid, lds, st); break;
+    case 3: if constexpr (kMax >= 3) return pair_launch<3, GATEUP, S, P, DT>(a, grid, lds, st); break;
+    case 4: if constexpr (kMax >= 4) return pair_launch<4, GATEUP, S, P, DT>(a, grid, lds, st); break;
+    case 5: if constexpr (kMax >= 5) return pair_launch<5, GATEUP, S, P, DT>(a, grid, lds, st); break;
+    case 6: if constexpr (kMax >= 6) return pair_launch<6, GATEUP, S, P, DT>(a, grid, lds, st); break;
     default: break;
   }
   return hipErrorNotSupported;
 }
 
-template <bool GATEUP, int P>
+template <bool GATEUP, int P, int DT>
 hipError_t pair_dispatch(const PairArgs& a, int S, int uc, int grid, int64_t lds, hipStream_t st) {
-  if (S == 1) return pair_dispatch_s<GATEUP, 1, P>(a, uc, grid, lds, st);
-  if (S == 2) return pair_dispatch_s<GATEUP, 2, P>(a, uc, grid, lds, st);
-  if (S == 4) return pair_dispatch_s<GATEUP, 4, P>(a, uc, grid, lds, st);
+  if (S == 1) return pair_dispatch_s<GATEUP, 1, P, DT>(a, uc, grid, lds, st);
+  if (S == 2) return pair_dispatch_s<GATEUP, 2, P, DT>(a, uc, grid, lds, st);
+  if (S == 4) return pair_dispatch_s<GATEUP, 4, P, DT>(a, uc, grid, lds, st);
   return hipErrorNotSupported;
 }
 
@@ -464,7 +484,8 @@ hipError_t pair_stage(const MlpArgs& m, hipStream_t st) {
   const int64_t K = GATEUP ? m.hidden : m.inter;
   const int64_t R = GATEUP ? m.inter : m.hidden;
   const bool norm = GATEUP && m.norm_w != nullptr;
-  if (m.dtype != kBF16 || !pair_plan(m.n, K, R, GATEUP, norm, a, grid, lds, S, uc)) return hipErrorNotSupported;
+  if ((m.dtype != kBF16 && m.dtype != kF16) || !pair_plan(m.n, K, R, GATEUP, norm, m.dtype, a, grid, lds, S, uc))
+    return hipErrorNotSupported;
   a.x = static_cast<const uint16_t*>(GATEUP ? m.x : m.tmp);
   a.w0 = GATEUP ? m.gate : m.down;
   a.s0 = GATEUP ? m.gate_scale : m.down_scale;
@@ -475,8 +496,11 @@ hipError_t pair_stage(const MlpArgs& m, hipStream_t st) {
   a.norm_w = norm ? static_cast<const uint16_t*>(m.norm_w) : nullptr;
   a.eps = m.eps;
   a.xn = norm ? static_cast<uint16_t*>(m.xn) : nullptr;
-  return m.n <= 2 ? pair_dispatch<GATEUP, 1>(a, S, uc, grid, lds, st)
-                  : pair_dispatch<GATEUP, 2>(a, S, uc, grid, lds, st);
+  if (m.dtype == kF16)
+    return m.n <= 2 ? pair_dispatch<GATEUP, 1, kF16>(a, S, uc, grid, lds, st)
+                    : pair_dispatch<GATEUP, 2, kF16>(a, S, uc, grid, lds, st);
+  return m.n <= 2 ? pair_dispatch<GATEUP, 1, kBF16>(a, S, uc, grid, lds, st)
+                  : pair_dispatch<GATEUP, 2, kBF16>(a, S, uc, grid, lds, st);
 }
 
 bool aligned16_pair(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -486,13 +510,15 @@ bool aligned16_pair(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15
 bool rowpair_enabled() { return option(kOptRowpair) != 0; }
 
 bool rowpair_supported(const MlpArgs& m, int stage) {
-  if (m.dtype != kBF16) return false;
+  if (m.dtype != kBF16 && m.dtype != kF16) return false;
   PairArgs a;
   int grid = 0, S = 0, uc = 0;
   int64_t lds = 0;
-  if ((stage & kStageGateUp) && !pair_plan(m.n, m.hidden, m.inter, true, m.norm_w != nullptr, a, grid, lds, S, uc))
+  if ((stage & kStageGateUp) &&
+      !pair_plan(m.n, m.hidden, m.inter, true, m.norm_w != nullptr, m.dtype, a, grid, lds, S, uc))
     return false;
-  if ((stage & kStageDown) && !pair_plan(m.n, m.inter, m.hidden, false, false, a, grid, lds, S, uc)) return false;
+  if ((stage & kStageDown) && !pair_plan(m.n, m.inter, m.hidden, false, false, m.dtype, a, grid, lds, S, uc))
+    return false;
   const void* p16[] = {m.x, m.gate, m.up, m.down, m.tmp, m.norm_w, m.xn};
   for (const void* p : p16)
     if (p && !aligned16_pair(p)) return false;

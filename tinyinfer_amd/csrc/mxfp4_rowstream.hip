@@ -441,13 +441,14 @@ bool row_plan(int64_t M, int64_t K, int64_t R, bool gateup, bool norm, int dtype
   // down: at most 3 chunks per wave where the split allows it (8B down, 6
   // chunks: 3 + 3 measured 6.36 us against 7.38 us whole and 7.22 us over four
   // waves); gate_up: whole rows (3 + 3 split measured no faster)
-  const int ucpref = gateup ? ucmax : 3;
+  const int ucpref = gateup ? ucmax : std::min(3, ucmax);
   for (int s = 1; S == 0 && s <= smax; s *= 2)
     if ((nc + s - 1) / s <= ucpref) S = s;
   for (int s = 1; S == 0 && s <= smax; s *= 2)
     if ((nc + s - 1) / s <= ucmax) S = s;
   if (S == 0 || S > nc) return false;
   uc = (nc + S - 1) / S;
+  if (uc > ucmax) return false;              // no kernel instantiated for it
   grid = (int)std::min<int64_t>(cus, (R * S + kRW - 1) / kRW);
   const int64_t nslots = (int64_t)grid * (kRW / S);
   a.K = (int)K;
