@@ -9,7 +9,8 @@ to the activation dtype): a few bf16 ulps. The shapes are chosen for the
 kernel's edge cases: waves with no K segment or a partial last unit, units
 spanning two row-group parts, fewer row groups than CUs and many row groups
 per workgroup, scale bytes outside the hardware conversion's exact range, and
-fp16 activations."""
+fp16 activations (fp16 MFMAs, fp16-subnormal weights, and the exact hi + lo
+form for scale bytes below fp16's range)."""
 
 import numpy as np
 import pytest
@@ -131,6 +132,38 @@ def test_stream_fp16_activations(capi):
     banner("stream fp16")
     x, mats = make_case(4, 1024, 3072, seed=31, dtype=torch.float16)
     run_stages(capi, x, mats, "fp16")
+
+
+@pytest.mark.parametrize("m", [3, 8])
+def test_stream_fp16_qwen3_8b(capi, m):
+    banner(f"stream fp16 8B m={m}")
+    x, mats = make_case(m, 4096, 12288, seed=33 + m, dtype=torch.float16)
+    run_stages(capi, x, mats, f"fp16 8B m={m}")
+
+
+def test_stream_fp16_scale_paths(capi):
+    """fp16 with scale bytes 104..113 (fp16-subnormal weights, fp16 MFMAs) and
+    below 104 (those units on exact bf16 weights against the activations'
+    bf16 hi and lo parts): every other output within the bar, the rows that
+    read only such a block exact to one fp16 unit."""
+    from tests.test_gpu_gemm import _isolate_block, _ulps_f16
+    banner("stream fp16 scale paths")
+    x, mats = make_case(5, 2048, 6144, seed=79, dtype=torch.float16)
+    gp, gs, up, us, dp, ds = [np.array(a) for a in mats]
+    gs[40, 3] = 90
+    us[1500, 20] = 95
+    rows = {5: 104, 333: 109, 600: 103, 1000: 113}
+    for row, byte in rows.items():
+        _isolate_block(dp, ds, [row], 7, byte)
+    mats = [gp, gs, up, us, dp, ds]
+    run_stages(capi, x, mats, "fp16 scale paths", cols=[c for c in range(2048) if c not in rows])
+    xd, md = to_dev(x, mats)
+    h_ref = h_semantics(x, gp, gs, up, us)
+    o = capi.down(h_ref.cuda(), md[4], md[5], path=SKINNY).cpu()
+    o_ref = down_semantics(h_ref, dp, ds)
+    for row in rows:
+        assert o_ref[:, row].float().abs().max() > 0
+        assert _ulps_f16(o[:, row], o_ref[:, row]) <= 1, row
 
 
 def test_stream_full_call_matches_stages(capi):

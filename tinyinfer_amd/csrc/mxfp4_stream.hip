@@ -119,8 +119,10 @@ __device__ __forceinline__ void issue_unit(const StreamArgs& a, int rg, int part
 }
 
 // Multiply one unit's items into acc (FAST: every scale byte in the
-// hardware-exact range; chosen once outside this body so each conversion
-// sits in the same basic block as its MFMA).  Every item goes through the
+// hardware-exact range -- for fp16 activations e8m0_f16_ok, the weights then
+// converted to fp16 on fp16 MFMAs, otherwise exact bf16 weights against the
+// activations' exact bf16 hi and lo parts; chosen once outside this body so
+// each conversion sits in the same basic block as its MFMA).  Every item goes through the
 // MFMA: a branch around the slots outside the unit would leave some loads
 // unconsumed on one path, and the compiler then drains the whole load queue
 // (vmcnt(0)) before the next issue, which serialises the pipeline.  FULL
@@ -142,11 +144,14 @@ __device__ __forceinline__ void mma_unit(int nu, const u32x4_t (&wv)[(GATEUP ? 2
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const uint32_t wq = live ? wv[k][t] : 0u;           // e2m1 code 0 is +0
-        const u32x4_t wa = FAST ? dq8_bf16_fast(wq, sb[k]) : dq8_bf16_exact(wq, sb[k]);
+        const u32x4_t wa = !FAST ? dq8_bf16_exact(wq, sb[k])
+                                 : DT == kBF16 ? dq8_bf16_fast(wq, sb[k]) : dq8_f16_fast(wq, sb[k]);
         const u32x4_t xr = xf(live ? sg : 0, t);
         const u32x4_t xb = live ? xr : u32x4_t{0u, 0u, 0u, 0u};   // 0 * (inf or nan in x) stays out
         if constexpr (DT == kBF16) {
           acc[mat] = mfma16x16x32(wa, xb, acc[mat]);
+        } else if constexpr (FAST) {
+          acc[mat] = mfma16x16x32_f16(wa, xb, acc[mat]);
         } else {
           u32x4_t xh, xlo;
           f16x8_split_bf16(xb, xh, xlo);
@@ -177,7 +182,7 @@ __device__ __forceinline__ void compute_unit(const StreamArgs& a, int wave, int 
     const int sg = k - mat * SPU;
     const uint8_t* srow = scl + ((li * kMats + mat) * 8 + r8) * a.ss_stride;
     sb[k] = sg < nu ? (uint32_t)srow[(s0 + sg) * 8 + q8] : 127u;
-    ok = ok && e8m0_fast_ok(sb[k]);
+    ok = ok && (DT == kBF16 ? e8m0_fast_ok(sb[k]) : e8m0_f16_ok(sb[k]));
   }
   if (wave_all(ok)) {
     if (nu == SPU) mma_unit<DT, SPU, GATEUP, true, true>(nu, wv, sb, xf, acc);
