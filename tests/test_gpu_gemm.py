@@ -162,6 +162,27 @@ def test_gemm_fp16_scales_outside_fp16_range(capi):
         assert _ulps_f16(o[:, row], o_ref[:, row]) <= 1, row
 
 
+def test_gemm_fp16_infinite_activation_on_the_hi_lo_path(capi):
+    """An infinite fp16 activation on the exact hi + lo path (every down tile
+    sent there by one scale byte below fp16's range per row) multiplies as
+    IEEE has it: +-inf where its weight is nonzero, NaN where it is zero, as in
+    the oracle; the other tokens stay finite and within the bar."""
+    banner("gemm fp16 inf activation, hi/lo path")
+    x, mats = make_case(160, 1024, 2048, seed=95, dtype=torch.float16)
+    gp, gs, up, us, dp, ds = [np.array(a) for a in mats]
+    ds[:, 0] = 103
+    h_ref = h_semantics(x, gp, gs, up, us)
+    h_ref[0, 100] = float("inf")
+    dpt, dst = torch.from_numpy(dp).cuda(), torch.from_numpy(ds).cuda()
+    o = capi.down(h_ref.cuda(), dpt, dst, path=GEMM).cpu().float()
+    o_ref = down_semantics(h_ref, dp, ds).float()
+    assert torch.equal(torch.isnan(o[0]), torch.isnan(o_ref[0]))
+    assert torch.equal(torch.isinf(o[0]), torch.isinf(o_ref[0])) and torch.isinf(o_ref[0]).any()
+    inf = torch.isinf(o_ref[0])
+    assert torch.equal(torch.sign(o[0][inf]), torch.sign(o_ref[0][inf]))
+    check_close(o[1:].to(torch.float16), o_ref[1:].to(torch.float16), "finite tokens")
+
+
 def test_gemm_deterministic_and_full_call(capi):
     """Two calls give the same bits; the full entry point equals its stages."""
     banner("gemm determinism")

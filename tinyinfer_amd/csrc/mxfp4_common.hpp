@@ -198,7 +198,10 @@ __device__ __forceinline__ u32x2_t with_residual4(u32x2_t v, const uint16_t* res
   return o;
 }
 
-// fp16x8 (as 4 dwords) -> exact bf16 hi/lo split: x = hi + lo with both bf16.
+// fp16x8 (as 4 dwords) -> exact bf16 hi/lo split: x = hi + lo with both bf16
+// (fp16's 11 significant bits over two 8-bit halves).  An infinite or NaN x
+// goes whole into hi with lo = 0, so w * hi + w * lo is w * x as IEEE has it
+// (inf - inf would make lo a NaN).
 __device__ __forceinline__ void f16x8_split_bf16(u32x4_t v, u32x4_t& hi, u32x4_t& lo) {
   f16x8_t h = __builtin_bit_cast(f16x8_t, v);
   bf16x8_t a, c;
@@ -207,7 +210,8 @@ __device__ __forceinline__ void f16x8_split_bf16(u32x4_t v, u32x4_t& hi, u32x4_t
     float f = static_cast<float>(h[j]);
     __bf16 t = static_cast<__bf16>(f);
     a[j] = t;
-    c[j] = static_cast<__bf16>(f - static_cast<float>(t));
+    const float r = f - static_cast<float>(t);
+    c[j] = static_cast<__bf16>(r == r ? r : 0.f);
   }
   hi = __builtin_bit_cast(u32x4_t, a);
   lo = __builtin_bit_cast(u32x4_t, c);
