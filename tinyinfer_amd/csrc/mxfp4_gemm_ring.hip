@@ -1,4 +1,4 @@
-// Tiled MXFP4 MLP GEMM for prefill (bf16 activations, K a multiple of 512):
+// Tiled MXFP4 MLP GEMM for prefill (bf16 or fp16 activations, K a multiple of 512):
 // a three-stage LDS ring fed by direct-to-LDS loads.
 //
 // Replaces the reference's per-token GEMV kernels mlp_stage1_mxfp4 /

@@ -85,7 +85,7 @@ hipError_t launch_skinny_mlp(const MlpArgs& a, int stage, hipStream_t stream);
 // Tiled MFMA GEMM path (n >= 128 preferred; any n >= 1 is correct).
 hipError_t launch_gemm_mlp(const MlpArgs& a, int stage, hipStream_t stream);
 
-// Prefill GEMM with a three-stage direct-to-LDS ring (bf16 activations, the
+// Prefill GEMM with a three-stage direct-to-LDS ring (bf16 or fp16, the
 // stage's K a multiple of 512, 16-byte aligned scale rows); launch_gemm_mlp
 // serves the other GEMM-path calls.
 bool gemm_ring_supported(const MlpArgs& a, int stage);
@@ -108,14 +108,14 @@ bool rowstream_enabled();
 bool rowstream_supported(const MlpArgs& a, int stage);
 hipError_t launch_rowstream_mlp(const MlpArgs& a, int stage, hipStream_t stream);
 
-// Row-pair kernels for 2..4 tokens (bf16): each load reads 512 B of each of
+// Row-pair kernels for 2..4 tokens: each load reads 512 B of each of
 // two weight rows, one MFMA serves two tokens.  rowpair_supported() says
 // whether the call fits; rowpair_enabled() is false when TINYINFER_ROWPAIR=0.
 bool rowpair_enabled();
 bool rowpair_supported(const MlpArgs& a, int stage);
 hipError_t launch_rowpair_mlp(const MlpArgs& a, int stage, hipStream_t stream);
 
-// Split-K tile kernels for up to 64 tokens (bf16, K % 1024 == 0): a workgroup
+// Split-K tile kernels for up to 64 tokens (K % 1024 == 0): a workgroup
 // owns one 1024-element K range (its activations staged once in LDS) and
 // streams 16-row weight groups through MFMA; a reduce launch adds the K
 // ranges in order and applies the epilogue (gate_up in one launch, partials

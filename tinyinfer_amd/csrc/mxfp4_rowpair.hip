@@ -1,4 +1,4 @@
-// Row-pair streaming MXFP4 GEMV for 2..4 tokens (bf16): one kernel per MLP
+// Row-pair streaming MXFP4 GEMV for 2..4 tokens: one kernel per MLP
 // stage, the same contract as the row-streaming kernel (mxfp4_rowstream.hip)
 // and the 8-row stream kernel (mxfp4_stream.hip) for the reference's
 // per-token GEMV kernels mlp_stage1_mxfp4 / mlp_stage2_mxfp4

@@ -1,4 +1,4 @@
-// Split-K tile kernels for small batches (up to 64 bf16 tokens): the
+// Split-K tile kernels for small batches (up to 64 bf16 or fp16 tokens): the
 // reference's per-token GEMV stages mlp_stage1_mxfp4 / mlp_stage2_mxfp4
 // (tinyinfer/csrc/mlp_fp4.cu:79-142, 365-426) for a batch whose activations
 // are too many for the decode kernels' registers (or whose K they decline,
