@@ -73,19 +73,24 @@ def test_residual_torch_extension(capi):
         ext.mlp_forward_mxfp4_residual(xd, *md, res[:2].contiguous())
 
 
-@pytest.mark.parametrize("m,k,r", [(1, 4096, 6144), (7, 4096, 4096), (200, 2048, 2048), (3, 1024, 151936),
-                                   (96, 1536, 512), (16, 4096, 4096), (48, 2048, 2048)])
-def test_linear_against_exact_sums(capi, m, k, r):
-    banner(f"linear m={m} k={k} r={r}")
+@pytest.mark.parametrize("m,k,r,dtype", [
+    (1, 4096, 6144, torch.bfloat16), (7, 4096, 4096, torch.bfloat16), (200, 2048, 2048, torch.bfloat16),
+    (3, 1024, 151936, torch.bfloat16), (96, 1536, 512, torch.bfloat16), (16, 4096, 4096, torch.bfloat16),
+    (48, 2048, 2048, torch.bfloat16),
+    # fp16 activations through the same kernel families
+    (1, 4096, 6144, torch.float16), (2, 4096, 4096, torch.float16), (5, 2048, 2048, torch.float16),
+    (16, 4096, 4096, torch.float16), (300, 2048, 2048, torch.float16)])
+def test_linear_against_exact_sums(capi, m, k, r, dtype):
+    banner(f"linear m={m} k={k} r={r} {dtype}")
     g = torch.Generator().manual_seed(k + r)
     w = torch.randn(r, k, generator=g) * 0.02
     p, s = ox.quantize_chunk(w)
-    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    x = torch.randn(m, k, generator=g).to(dtype)
     pd, sd = torch.from_numpy(p).cuda(), torch.from_numpy(s).cuda()
     y = capi.linear(x.cuda(), pd, sd)
     torch.cuda.synchronize()
     check_close(y.cpu(), down_semantics(x, p, s), f"linear {m}x{k}->{r}")
-    res = torch.randn(m, r, generator=g).to(torch.bfloat16).cuda()
+    res = torch.randn(m, r, generator=g).to(dtype).cuda()
     yr = capi.linear(x.cuda(), pd, sd, residual=res)
     torch.cuda.synchronize()
     assert torch.equal(yr.view(torch.int16), _added(res, y).view(torch.int16))
