@@ -71,14 +71,16 @@ def test_rmsnorm_torch_extension(capi):
 
 
 @pytest.mark.parametrize("m,h,i,path,dtype", [
-    (1, 1024, 3072, AUTO, torch.bfloat16),        # stream kernels, norm in gate_up's prologue
-    (4, 2048, 6144, AUTO, torch.float16),         # the same, fp16
+    (1, 1024, 3072, AUTO, torch.bfloat16),        # row kernels, norm in gate_up's prologue
+    (1, 4096, 12288, AUTO, torch.float16),        # the same, fp16 (x normalized and kept as fp16)
+    (2, 2048, 6144, AUTO, torch.float16),         # row-pair kernels, norm in the prologue, fp16
+    (4, 2048, 6144, AUTO, torch.float16),         # stream kernels (gate_up) and row-pair (down), fp16
     (8, 1024, 3072, SKINNY, torch.bfloat16),      # stream kernels at their token limit
     (8, 2560, 3072, SKINNY, torch.bfloat16),      # x beyond the preload registers: norm from LDS
     (2, 1024, 3072, DECODE, torch.bfloat16),      # norm kernel + fused decode kernel
     (24, 1024, 1536, SKINNY, torch.bfloat16),     # norm kernel + skinny kernels
     (300, 1024, 1536, GEMM, torch.bfloat16),      # norm kernel + ring GEMM
-    (130, 1024, 1536, GEMM, torch.float16),       # norm kernel + register-staged GEMM (fp16)
+    (130, 1024, 1536, GEMM, torch.float16),       # norm kernel + ring GEMM, fp16
 ])
 def test_decoder_mlp_half(capi, m, h, i, path, dtype):
     banner(f"rmsnorm mlp m={m} h={h} i={i} path={path} {dtype}")
