@@ -251,7 +251,8 @@ int tinyinfer_mxfp4_decode_reset(void);
  * Tuning options, by the name of the environment variable that sets each at
  * load (TINYINFER_ROWSTREAM, TINYINFER_ROWPAIR, TINYINFER_TILE,
  * TINYINFER_TILE_GU, TINYINFER_ROW_SPLIT_GATEUP, TINYINFER_ROW_SPLIT_DOWN,
- * TINYINFER_GEMM_RING, TINYINFER_RING_KSPLIT, TINYINFER_RING_WR_GU / _DN,
+ * TINYINFER_GEMM_RING, TINYINFER_RING_KSPLIT, TINYINFER_RING_TAIL,
+ * TINYINFER_RING_WR_GU / _DN,
  * TINYINFER_RING_NW_GU / _DN, TINYINFER_SKINNY_NW, TINYINFER_STREAM_SPU_GU /
  * _DN, TINYINFER_STREAM_XREG, TINYINFER_WORKSPACE_MB, TINYINFER_DECODE_SPIN).
  * The environment is read once, at the first call that needs an option; set

@@ -12,7 +12,8 @@ its exact hi + lo path for scale bytes below fp16's range),
 bit-reproducibility, and the
 split-K form of the ring kernels (fp32 partials over K ranges summed in a
 fixed order by a reduce kernel) that runs when the output tiles alone would
-leave CUs idle.""" 
+leave CUs idle, for every tile or for the tiles past the last full round of
+workgroups only (the tail split)."""  
 
 import os
 
@@ -230,6 +231,65 @@ def test_gemm_split_deterministic(capi):
     torch.cuda.synchronize()
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
     check_close(a.cpu(), c.cpu().float(), "split vs unsplit")
+
+
+@pytest.mark.parametrize("m,dtype,row0", [
+    (300, torch.bfloat16, 10880),    # 288 gate_up tiles: 255 whole + 33 in 7 K ranges
+    (257, torch.bfloat16, 10880),    # the same split, one token in the last token tile
+    (384, torch.float16, 10880),
+])
+def test_gemm_tail_split_qwen3_8b(capi, m, dtype, row0):
+    """Qwen3-8B gate_up at token counts whose tiles leave the last round of
+    workgroups part-empty: the tiles past the last full round are split over
+    K (TINYINFER_RING_TAIL), where the cost model prefers that to splitting
+    every tile or none.  Both stages match the oracle; the output rows of the
+    whole tiles are bit-identical to the unsplit kernel's
+    (TINYINFER_RING_KSPLIT=1), the split band within the tolerance, and the
+    split call is bit-reproducible."""
+    banner(f"gemm tail split qwen3-8b m={m} {dtype}")
+    x, mats = make_case(m, 4096, 12288, seed=90 + m, dtype=dtype)
+    run_gemm_stages(capi, x, mats, f"8B m={m} tail split")
+    xd, md = to_dev(x, mats)
+    a = capi.gate_up(xd, *md[:4], path=GEMM)
+    b = capi.gate_up(xd, *md[:4], path=GEMM)
+    with capi.option("TINYINFER_RING_KSPLIT", 1):       # every tile whole
+        c = capi.gate_up(xd, *md[:4], path=GEMM)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert torch.equal(a[:, :row0].view(torch.int16), c[:, :row0].view(torch.int16))
+    assert not torch.equal(a[:, row0:].view(torch.int16), c[:, row0:].view(torch.int16)), "band not split"
+    check_close(a[:, row0:].cpu(), c[:, row0:].cpu().float(), "split band vs unsplit")
+
+
+def test_gemm_tail_split_graph_replays(capi):
+    """A graph captured on a stream that already ran the tail-split call
+    replays it bit-identically, with eager work between replays."""
+    banner("gemm tail split graph replays")
+    m = 300
+    x, mats = make_case(m, 4096, 12288, seed=45)
+    xd, md = to_dev(x, mats)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    out = torch.empty((m, 4096), dtype=torch.bfloat16, device="cuda")
+    tmp = torch.empty((m, 12288), dtype=torch.bfloat16, device="cuda")
+    with torch.cuda.stream(s):
+        capi.mlp_forward(xd, *md, out=out, tmp=tmp, path=GEMM)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    eager = out.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        capi.mlp_forward(xd, *md, out=out, tmp=tmp, path=GEMM)
+    for _ in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), eager.view(torch.int16))
+        capi.mlp_forward(xd[:200].contiguous(), *md, path=GEMM)
+        torch.cuda.synchronize()
+    del g
+    check_close(eager.cpu(), om.mlp_kernel_semantics(x, *mats), "tail split full call")
 
 
 def test_gemm_split_k_graph_replays(capi):

@@ -34,6 +34,7 @@
 // (a permutation of K shared by both operands leaves each dot product
 // unchanged).  A lane's W bytes for the step are then one 16-byte run under
 // one scale byte, and its X bytes one 64-byte run.
+#include <mutex>
 #include <type_traits>
 #include <utility>
 
@@ -71,9 +72,12 @@ struct RingArgs {
   uint16_t* out;            // [M, N]
   int M, N, K;              // N: output rows
   int m_tiles, n_tiles;
-  float* ws;                // split K: fp32 partials [ksplit][M][NMAT * N]
-  int ksplit;               // K ranges per tile (1: no split)
+  float* ws;                // split K: fp32 partials [ksplit][M][NMAT * tail_n]
+  int ksplit;               // K ranges per split tile (1: no split)
   const uint16_t* res;      // down only: residual [M, N] added to out, or null
+  int nfull = 0;            // split kernel: tiles [0, nfull) run whole, the rest split
+  int tail_row0 = 0;        // first output row of the split tiles (a band of whole weight tiles)
+  int tail_n = 0;           // output rows from tail_row0 to N
 };
 
 // 64 lanes x 16 bytes from per-lane global addresses to 1 KB of LDS at l
@@ -108,7 +112,11 @@ __device__ __forceinline__ void tile_row(int tr, int row0, int N, int& mat, int&
 // SPLIT: the grid also splits K into ksplit ranges of whole 8-step blocks
 // (the scale staging's granularity); each workgroup writes its fp32 partial
 // tile to the workspace, and ring_reduce sums the ranges in a fixed order and
-// applies the epilogue.  Used when the tiles alone would leave CUs idle.
+// applies the epilogue.  Used when the tiles alone would leave CUs idle: for
+// every tile (nfull = 0), or for the tiles past the last full round of
+// workgroups over the CUs (the first nfull workgroups run tiles [0, nfull)
+// whole, with the plain epilogue; the split ones are the band of output rows
+// from tail_row0, so their partials take ksplit * M * tail_n floats).
 // WR: waves along the weight rows (8 / WR along the tokens).  A wave holds
 // WB = 8 / WR blocks of 32 weight rows and kTT = BM / 32 / (8 / WR) blocks of
 // 32 tokens; fewer, wider weight blocks per wave read less LDS per MFMA (the
@@ -140,10 +148,14 @@ __global__ __launch_bounds__(NW * 64, 2) void gemm_ring_kernel(RingArgs a) {
   // tiles fastest, so the WGs sharing a weight tile run on one L2) -------
   const int nwg = gridDim.x;
   const int wg = blockIdx.x;
-  int logical = wg;
-  if ((nwg & 7) == 0) logical = (wg & 7) * (nwg >> 3) + (wg >> 3);
-  const int tile = SPLIT ? logical / a.ksplit : logical;
-  const int ks = SPLIT ? logical - tile * a.ksplit : 0;
+  // whole tiles first (workgroups [0, nfull)), then the split ones; each XCD
+  // walks a contiguous range of either
+  auto xcd_walk = [](int w, int n) { return (n & 7) == 0 ? (w & 7) * (n >> 3) + (w >> 3) : w; };
+  const int nfull = SPLIT ? a.nfull : 0;
+  const int logical = wg < nfull ? xcd_walk(wg, nfull) : nfull + xcd_walk(wg - nfull, nwg - nfull);
+  const bool part = SPLIT && logical >= nfull;          // this workgroup writes partials
+  const int tile = part ? nfull + (logical - nfull) / a.ksplit : logical;
+  const int ks = part ? (logical - nfull) - (tile - nfull) * a.ksplit : 0;
   const int n_tile = tile / a.m_tiles;
   const int m_tile = tile - n_tile * a.m_tiles;
   const int row0 = n_tile * kRowsOut;
@@ -151,8 +163,8 @@ __global__ __launch_bounds__(NW * 64, 2) void gemm_ring_kernel(RingArgs a) {
   const int M = a.M, N = a.N, K = a.K;
   // K steps [kbeg, kend) of this workgroup
   const int nblk = K / (8 * kBK);
-  const int kbeg = SPLIT ? 8 * (ks * nblk / a.ksplit) : 0;
-  const int kend = SPLIT ? 8 * ((ks + 1) * nblk / a.ksplit) : K / kBK;
+  const int kbeg = part ? 8 * (ks * nblk / a.ksplit) : 0;
+  const int kend = part ? 8 * ((ks + 1) * nblk / a.ksplit) : K / kBK;
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -337,13 +349,14 @@ __global__ __launch_bounds__(NW * 64, 2) void gemm_ring_kernel(RingArgs a) {
 
   // ---- epilogue --------------------------------------------------------
   // acc[b][t][v]: token tok0 + xtr[t], tile row block base + 8 (v/4) + 4 j + (v%4)
-  if constexpr (SPLIT) {
-    // fp32 partials: [ks][token][mat * N + row], four consecutive rows per store
+  if (part) {
+    // fp32 partials: [ks][token][mat * tail_n + row - tail_row0], four
+    // consecutive rows per store
 #pragma unroll
     for (int t = 0; t < kTT; ++t) {
       const int tok = tok0 + xtr[t];
       if (tok >= M) continue;
-      float* wrow = a.ws + ((int64_t)ks * M + tok) * (NMAT * N);
+      float* wrow = a.ws + ((int64_t)ks * M + tok) * (NMAT * a.tail_n);
 #pragma unroll
       for (int b = 0; b < WB; ++b) {
 #pragma unroll
@@ -351,7 +364,7 @@ __global__ __launch_bounds__(NW * 64, 2) void gemm_ring_kernel(RingArgs a) {
           const int orow = row0 + (NMAT == 2 ? wr * (kRowsW / 2) + (b % (WB / 2)) * 32 : wr * kRowsW + b * 32) +
                            8 * g + 4 * j;
           if (orow >= N) continue;
-          const int col = (NMAT == 2 ? (b / (WB / 2)) * N : 0) + orow;
+          const int col = (NMAT == 2 ? (b / (WB / 2)) * a.tail_n : 0) + orow - a.tail_row0;
           *reinterpret_cast<f32x4_t*>(wrow + col) =
               f32x4_t{acc[b][t][4 * g], acc[b][t][4 * g + 1], acc[b][t][4 * g + 2], acc[b][t][4 * g + 3]};
         }
@@ -384,28 +397,31 @@ __global__ __launch_bounds__(NW * 64, 2) void gemm_ring_kernel(RingArgs a) {
   }
 }
 
-// out[m][n] = epilogue(sum over ks of ws[ks][m][n] (and [N + n] for up)), in
-// ks order; four outputs per thread.
+// out[m][row0 + n] = epilogue(sum over ks of ws[ks][m][n] (and [nt + n] for
+// up)), in ks order, for the nt output rows from row0; four outputs per
+// thread.
 template <int NMAT, int DT>
 __global__ __launch_bounds__(256) void ring_reduce(const float* __restrict__ ws, uint16_t* out,
-                                                   const uint16_t* res, int M, int N, int ksplit) {
+                                                   const uint16_t* res, int M, int N, int ksplit, int row0,
+                                                   int nt) {
   const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;   // group of 4 outputs
-  const int64_t total = (int64_t)M * N / 4;
+  const int64_t total = (int64_t)M * nt / 4;
   if (q >= total) return;
-  const int64_t m = q / (N / 4);
-  const int n = (int)(q - m * (N / 4)) * 4;
+  const int64_t m = q / (nt / 4);
+  const int n = (int)(q - m * (nt / 4)) * 4;
   f32x4_t g = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
   for (int ks = 0; ks < ksplit; ++ks) {
-    const float* row = ws + ((int64_t)ks * M + m) * (NMAT * N);
+    const float* row = ws + ((int64_t)ks * M + m) * (NMAT * nt);
     g += *reinterpret_cast<const f32x4_t*>(row + n);
-    if constexpr (NMAT == 2) u += *reinterpret_cast<const f32x4_t*>(row + N + n);
+    if constexpr (NMAT == 2) u += *reinterpret_cast<const f32x4_t*>(row + nt + n);
   }
   float v[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) v[e] = NMAT == 2 ? silu_f32(g[e]) * u[e] : g[e];
   const uint32_t lo = (uint32_t)f32_to_act<DT>(v[0]) | ((uint32_t)f32_to_act<DT>(v[1]) << 16);
   const uint32_t hi = (uint32_t)f32_to_act<DT>(v[2]) | ((uint32_t)f32_to_act<DT>(v[3]) << 16);
-  *reinterpret_cast<u32x2_t*>(out + m * N + n) = with_residual4<DT>(u32x2_t{lo, hi}, res, m * N + n);
+  const int64_t o = m * N + row0 + n;
+  *reinterpret_cast<u32x2_t*>(out + o) = with_residual4<DT>(u32x2_t{lo, hi}, res, o);
 }
 
 // Number of K ranges per output tile.  Cost model (microseconds): a tile's
@@ -415,20 +431,34 @@ __global__ __launch_bounds__(256) void ring_reduce(const float* __restrict__ ws,
 // launch.  The smallest split with the least cost wins; K ranges are whole
 // 8-step blocks, and the partials of all ranges fit the workspace limit.
 // The option TINYINFER_RING_KSPLIT=<n> forces n (clamped), for tuning.
-int ring_ksplit(const RingArgs& r, int bm, int nmat, int64_t tiles, int per_cu, size_t ws_limit) {
+// whole_per_cu: workgroups of the unsplit kernel that fit one CU at once.
+// With two, a CU that runs two tiles together takes ~1.75 tile times (both
+// share its matrix cores; Qwen3-8B gate_up, 128-token tiles: 384 tiles in
+// 118-128 us against 70.5 us for 192), not two rounds.
+int ring_ksplit(const RingArgs& r, int bm, int nmat, int64_t tiles, int per_cu, size_t ws_limit,
+                double* cost_out = nullptr, bool* forced = nullptr, int whole_per_cu = 1) {
   const int nblk = r.K / (8 * kBK);
   int cap = nblk < 32 ? nblk : 32;
   const size_t per_split = (size_t)r.M * nmat * r.N * sizeof(float);
   const size_t fit = per_split ? ws_limit / per_split : 0;
   if ((size_t)cap > fit) cap = (int)fit;
-  if (cap < 2) return 1;
-  if (const int v = option(kOptRingKsplit); v >= 1) return v < cap ? v : cap;
   // per_cu workgroups share a CU: each runs at 1 / per_cu of its rate
   const int64_t slots = 256 * per_cu;
   const double t_tile = 2.0 * bm * 256.0 * r.K / 5e6 * per_cu;
   const double ws_us_per_split = 8.0 * r.M * nmat * (double)r.N / 8e6;
   int best = 1;
   double best_cost = t_tile * (double)((tiles + slots - 1) / slots);
+  if (per_cu == 1 && whole_per_cu >= 2) {
+    const int64_t c = (tiles + 255) / 256;         // tiles per CU
+    best_cost = t_tile * (1.75 * (double)(c / 2) + (double)(c % 2));
+  }
+  if (cost_out) *cost_out = best_cost;
+  if (forced) *forced = false;
+  if (cap < 2) return 1;
+  if (const int v = option(kOptRingKsplit); v >= 1) {
+    if (forced) *forced = true;
+    return v < cap ? v : cap;
+  }
   for (int ks = 2; ks <= cap; ++ks) {
     const double rounds = (double)((tiles * ks + slots - 1) / slots);
     const double cost = t_tile * rounds / ks + ws_us_per_split * ks + 3.0;
@@ -437,7 +467,51 @@ int ring_ksplit(const RingArgs& r, int bm, int nmat, int64_t tiles, int per_cu, 
       best_cost = cost;
     }
   }
+  if (cost_out) *cost_out = best_cost;
   return best;
+}
+
+// Split of the tiles past the last full round only (RingArgs::nfull): the
+// first rounds of workgroups over the CUs run whole tiles, and the remaining
+// tiles (a band of whole weight-row tiles) are split into s K ranges so that
+// they fill one more round.  At Qwen3-8B gate_up and 512 tokens: 384 tiles =
+// 256 whole + 128 halves, where the whole-tile grid left half of its second
+// round empty.  Same cost model as ring_ksplit; s = 1 when it does not pay.
+struct TailSplit {
+  int nfull = 0;
+  int s = 1;
+  int row0 = 0;
+  double cost = 0.0;
+};
+TailSplit ring_tail_split(const RingArgs& r, int bm, int nmat, int rows_out, int64_t tiles, size_t ws_limit) {
+  TailSplit t;
+  const int64_t slots = 256;
+  if (option(kOptRingTail) == 0 || tiles <= slots || tiles % slots == 0 || r.m_tiles < 1) return t;
+  const int64_t rounds = tiles / slots;
+  const int64_t nfull = rounds * slots / r.m_tiles * r.m_tiles;
+  const int64_t ntail = tiles - nfull;
+  if (nfull < 1 || ntail < 1) return t;
+  const int nblk = r.K / (8 * kBK);
+  int64_t s = ((rounds + 1) * slots - nfull) / ntail;
+  s = s < nblk ? s : nblk;
+  s = s < 32 ? s : 32;
+  const int row0 = (int)(nfull / r.m_tiles) * rows_out;
+  const int64_t tail_n = (int64_t)r.N - row0;
+  if (tail_n <= 0) return t;
+  const size_t per_split = (size_t)r.M * nmat * (size_t)tail_n * sizeof(float);
+  while (s >= 2 && (size_t)s * per_split > ws_limit) --s;
+  if (s < 2) return t;
+  const double t_tile = 2.0 * bm * 256.0 * r.K / 5e6;
+  // whole rounds, the split round, the partials written and read back, the
+  // reduce launch and the extra round's pipeline fill (measured at 8B gate_up:
+  // 288 tiles = 255 whole + 33 in 7 ranges 1.40 tile times, 384 = 256 + 128
+  // halves 1.78)
+  t.cost = t_tile * (double)rounds + t_tile / (double)s + 8.0 * (double)s * r.M * nmat * (double)tail_n / 8e6 +
+           3.0 + 0.1 * t_tile;
+  t.nfull = (int)nfull;
+  t.s = (int)s;
+  t.row0 = row0;
+  return t;
 }
 
 // A caller-provided workspace (fixed != null) of fixed_bytes is used instead
@@ -455,11 +529,43 @@ hipError_t launch_ring(RingArgs r, hipStream_t st, FixedWs fixed) {
   r.n_tiles = (r.N + kRowsOut - 1) / kRowsOut;
   const int64_t tiles = (int64_t)r.m_tiles * r.n_tiles;
   if (tiles > 0x7fffffff / 32) return hipErrorInvalidValue;
+  const size_t ws_limit = fixed.ptr ? fixed.bytes : workspace_limit();
+  // how many unsplit workgroups one CU holds at once (registers and LDS),
+  // asked once per kernel
+  static std::once_flag occ_once;
+  static int whole_per_cu = 1;
+  std::call_once(occ_once, [] {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &n, reinterpret_cast<const void*>(gemm_ring_kernel<NMAT, BM, false, WR, NW, DT>), NW * 64, C::kLds) ==
+            hipSuccess &&
+        n > 0)
+      whole_per_cu = n;
+    else
+      (void)hipGetLastError();
+  });
+  double uniform_cost = 0.0;
+  bool forced = false;
   const int ksplit_want =
-      ring_ksplit(r, BM, NMAT, tiles, NW == 4 ? 2 : 1, fixed.ptr ? fixed.bytes : workspace_limit());
+      ring_ksplit(r, BM, NMAT, tiles, NW == 4 ? 2 : 1, ws_limit, &uniform_cost, &forced, whole_per_cu);
   int ksplit = 1;
   r.ws = nullptr;
-  if (ksplit_want > 1) {
+  r.nfull = 0;
+  r.tail_row0 = 0;
+  r.tail_n = r.N;
+  // the tail split when the model prefers it to the best split of every tile
+  TailSplit t;
+  if (NW == 8 && !forced) t = ring_tail_split(r, BM, NMAT, kRowsOut, tiles, ws_limit);
+  if (t.s > 1 && t.cost < 0.97 * uniform_cost) {
+    const int tail_n = r.N - t.row0;
+    r.ws = fixed.ptr ? fixed.ptr : gemm_split_workspace((size_t)t.s * r.M * NMAT * tail_n * sizeof(float), st);
+    if (r.ws) {
+      ksplit = t.s;
+      r.nfull = t.nfull;
+      r.tail_row0 = t.row0;
+      r.tail_n = tail_n;
+    }
+  } else if (ksplit_want > 1) {
     r.ws = fixed.ptr ? fixed.ptr
                      : gemm_split_workspace((size_t)ksplit_want * r.M * NMAT * r.N * sizeof(float), st);
     if (r.ws) ksplit = ksplit_want;
@@ -475,10 +581,11 @@ hipError_t launch_ring(RingArgs r, hipStream_t st, FixedWs fixed) {
     return hipGetLastError();
   };
   if (ksplit == 1) return go(gemm_ring_kernel<NMAT, BM, false, WR, NW, DT>, tiles);
-  const hipError_t e = go(gemm_ring_kernel<NMAT, BM, true, WR, NW, DT>, tiles * ksplit);
+  const hipError_t e = go(gemm_ring_kernel<NMAT, BM, true, WR, NW, DT>, r.nfull + (tiles - r.nfull) * ksplit);
   if (e != hipSuccess) return e;
-  const int64_t groups = (int64_t)r.M * r.N / 4;
-  ring_reduce<NMAT, DT><<<(unsigned)((groups + 255) / 256), 256, 0, st>>>(r.ws, r.out, r.res, r.M, r.N, ksplit);
+  const int64_t groups = (int64_t)r.M * r.tail_n / 4;
+  ring_reduce<NMAT, DT><<<(unsigned)((groups + 255) / 256), 256, 0, st>>>(r.ws, r.out, r.res, r.M, r.N, ksplit,
+                                                                          r.tail_row0, r.tail_n);
   return hipGetLastError();
 }
 

@@ -68,6 +68,7 @@ enum Opt : int {
   kOptStreamXreg,       // TINYINFER_STREAM_XREG    1: gate_up activations in VGPRs
   kOptWorkspaceMB,      // TINYINFER_WORKSPACE_MB   limit of one split-K workspace buffer
   kOptDecodeSpin,       // TINYINFER_DECODE_SPIN    fused decode kernel's wait bound (poll rounds)
+  kOptRingTail,         // TINYINFER_RING_TAIL      1: ring GEMM splits only the tiles past the last full round
   kOptCount
 };
 int option(Opt o);

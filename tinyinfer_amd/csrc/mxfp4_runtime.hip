@@ -78,6 +78,7 @@ constexpr OptSpec kSpecs[kOptCount] = {
     {"TINYINFER_STREAM_XREG", 1, 0, 1, false},
     {"TINYINFER_WORKSPACE_MB", 512, 0, 1 << 20, false},
     {"TINYINFER_DECODE_SPIN", 1 << 20, 0, 1 << 30, false},
+    {"TINYINFER_RING_TAIL", 1, 0, 1, false},
 };
 
 bool valid_value(const OptSpec& s, int v) {
