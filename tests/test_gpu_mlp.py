@@ -142,10 +142,12 @@ def test_golden_fixture(capi):
         assert_parity(out, ref, f"golden path={path}")
 
 
-@pytest.mark.parametrize("m", [1, 256, 512, 2048])
+@pytest.mark.parametrize("m", [1, 256, 300, 512, 2048, 2176])
 def test_qwen3_8b_against_torch_fp32_reference(capi, m):
     """Full 8B shape (gate/up [12288,4096], down [4096,12288]); reference is a
-    torch fp32 GPU dequant-then-matmul built from plain torch ops."""
+    torch fp32 GPU dequant-then-matmul built from plain torch ops.  300 and
+    2176 tokens take the ring GEMM's tail split (gate_up at 300; both stages
+    at 2176, one token tile past 2048)."""
     from tinyinfer_amd.workloads import activations, quantized_weights
     banner(f"8B m={m}")
     mats = quantized_weights(4096, 12288, layer=0)
