@@ -125,7 +125,68 @@ __device__ __forceinline__ void tile_group_mma(const TileBuf& b, const uint8_t* 
   else tile_mma<MT, DT == kBF16 ? 1 : 3>(b, lds, tstride, acc);
 }
 
+// Two groups at once: each activation operand read from LDS serves both
+// groups' MFMAs (half the LDS reads of two tile_group_mma calls; the same
+// products and sums, so the same bits).  One form for both: the fast
+// conversion only when every scale byte of both groups allows it.
+template <int MT, int MODE>
+__device__ __forceinline__ void tile_mma_pair(const TileBuf& b0, const TileBuf& b1, const uint8_t* lds, int tstride,
+                                              f32x4_t (&acc0)[MT], f32x4_t (&acc1)[MT]) {
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int c = 0; c < kRangeLoads; ++c) {
+    const uint32_t s0 = tile_scale(b0, c), s1 = tile_scale(b1, c);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const u32x4_t w0 = MODE == 0   ? dq8_bf16_fast(b0.w[c][q], s0)
+                         : MODE == 2 ? dq8_f16_fast(b0.w[c][q], s0)
+                                     : dq8_bf16_exact(b0.w[c][q], s0);
+      const u32x4_t w1 = MODE == 0   ? dq8_bf16_fast(b1.w[c][q], s1)
+                         : MODE == 2 ? dq8_f16_fast(b1.w[c][q], s1)
+                                     : dq8_bf16_exact(b1.w[c][q], s1);
+      const int ch = (4 * c + g) * 4 + q;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const u32x4_t xb = *reinterpret_cast<const u32x4_t*>(lds + (16 * mt + n) * tstride + 16 * (ch ^ n));
+        if constexpr (MODE == 2) {
+          acc0[mt] = mfma16x16x32_f16(w0, xb, acc0[mt]);
+          acc1[mt] = mfma16x16x32_f16(w1, xb, acc1[mt]);
+        } else if constexpr (MODE == 3) {
+          u32x4_t xh, xl;
+          f16x8_split_bf16(xb, xh, xl);
+          acc0[mt] = mfma16x16x32(w0, xl, mfma16x16x32(w0, xh, acc0[mt]));
+          acc1[mt] = mfma16x16x32(w1, xl, mfma16x16x32(w1, xh, acc1[mt]));
+        } else {
+          acc0[mt] = mfma16x16x32(w0, xb, acc0[mt]);
+          acc1[mt] = mfma16x16x32(w1, xb, acc1[mt]);
+        }
+      }
+      // one quarter at a time: the compiler would otherwise hoist every
+      // quarter's operand reads and spill
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
 template <int MT, int DT>
+__device__ __forceinline__ void tile_pair_mma(const TileBuf& b0, const TileBuf& b1, const uint8_t* lds, int tstride,
+                                              f32x4_t (&acc0)[MT], f32x4_t (&acc1)[MT]) {
+  bool ok = true;
+#pragma unroll
+  for (int c = 0; c < kRangeLoads; ++c) {
+    ok = ok && (DT == kBF16 ? e8m0_fast_ok(tile_scale(b0, c)) : e8m0_f16_ok(tile_scale(b0, c)));
+    ok = ok && (DT == kBF16 ? e8m0_fast_ok(tile_scale(b1, c)) : e8m0_f16_ok(tile_scale(b1, c)));
+  }
+  if (wave_all(ok)) tile_mma_pair<MT, DT == kBF16 ? 0 : 2>(b0, b1, lds, tstride, acc0, acc1);
+  else tile_mma_pair<MT, DT == kBF16 ? 1 : 3>(b0, b1, lds, tstride, acc0, acc1);
+}
+
+// PAIR: every wave owns exactly two groups (ngroups = 2 * wpk * 8, the 8B down
+// stage at every token count): they are multiplied together, one LDS read
+// of each activation operand for both.  A kernel of its own, so that the
+// loop form's registers are not raised by it.
+template <int MT, int DT, bool PAIR>
 __global__ __launch_bounds__(kTThreads, 1) void tile_kernel(TileArgs a) {
   constexpr int kXPre = MT * 16 * (kRangeK / 8) / kTThreads;   // 16-byte x chunks per thread
   extern __shared__ __align__(16) uint8_t lds[];
@@ -164,14 +225,8 @@ __global__ __launch_bounds__(kTThreads, 1) void tile_kernel(TileArgs a) {
   asm volatile("" ::: "memory");
 
   const int nmr = a.nmat * a.R;
-  auto step = [&](TileBuf& b, int j, auto issue_tag) __attribute__((always_inline)) {
-    const int G = group_of(j);
-    f32x4_t acc[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    tile_group_mma<MT, DT>(b, lds, kTokenLds, acc);
-    if constexpr (decltype(issue_tag)::value) tile_issue(a, group_of(j + 2), kr, b);
-    // lane l holds rows 4 (l / 16) + v of the group, token 16 mt + l % 16
+  // lane l holds rows 4 (l / 16) + v of the group, token 16 mt + l % 16
+  auto store = [&](int G, const f32x4_t (&acc)[MT]) __attribute__((always_inline)) {
     const int rg = a.R / 16;
     const int m = G / rg;
     const int col = m * a.R + (G - m * rg) * 16 + 4 * (lane >> 4);
@@ -181,6 +236,25 @@ __global__ __launch_bounds__(kTThreads, 1) void tile_kernel(TileArgs a) {
       *reinterpret_cast<f32x4_t*>(a.ws + ((int64_t)kr * a.mpad + t) * nmr + col) = acc[mt];
     }
   };
+  auto step = [&](TileBuf& b, int j, auto issue_tag) __attribute__((always_inline)) {
+    const int G = group_of(j);
+    f32x4_t acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    tile_group_mma<MT, DT>(b, lds, kTokenLds, acc);
+    if constexpr (decltype(issue_tag)::value) tile_issue(a, group_of(j + 2), kr, b);
+    store(G, acc);
+  };
+  if constexpr (PAIR) {
+    // the wave's whole share is the two groups in flight
+    f32x4_t acc0[MT], acc1[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc0[mt] = acc1[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    tile_pair_mma<MT, DT>(b0, b1, lds, kTokenLds, acc0, acc1);
+    store(group_of(0), acc0);
+    store(group_of(1), acc1);
+    return;
+  }
   constexpr std::true_type kIssue{};
   constexpr std::false_type kLast{};
   // every load issued is a group the wave multiplies (tails peeled; an issue
@@ -387,7 +461,7 @@ bool aligned_tile(const void* p, uintptr_t n) { return (reinterpret_cast<uintptr
 template <int MT, int DT>
 hipError_t tile_launch(const TileArgs& a, int grid, hipStream_t st) {
   const int lds = MT * 16 * kTokenLds;
-  auto k = tile_kernel<MT, DT>;
+  auto k = a.ngroups == 2 * a.wpk * kTW ? tile_kernel<MT, DT, true> : tile_kernel<MT, DT, false>;
   if (lds > 64 * 1024 &&
       hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, lds) !=
           hipSuccess)
