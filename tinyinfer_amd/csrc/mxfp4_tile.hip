@@ -125,41 +125,41 @@ __device__ __forceinline__ void tile_group_mma(const TileBuf& b, const uint8_t* 
   else tile_mma<MT, DT == kBF16 ? 1 : 3>(b, lds, tstride, acc);
 }
 
-// Two groups at once: each activation operand read from LDS serves both
-// groups' MFMAs (half the LDS reads of two tile_group_mma calls; the same
-// products and sums, so the same bits).  One form for both: the fast
-// conversion only when every scale byte of both groups allows it.
-template <int MT, int MODE>
-__device__ __forceinline__ void tile_mma_pair(const TileBuf& b0, const TileBuf& b1, const uint8_t* lds, int tstride,
-                                              f32x4_t (&acc0)[MT], f32x4_t (&acc1)[MT]) {
+// NG groups at once: each activation operand read from LDS serves all NG
+// groups' MFMAs (1 / NG of the LDS reads of NG tile_group_mma calls; the
+// same products and sums, so the same bits).  One form for all: the fast
+// conversion only when every scale byte of every group allows it.
+template <int MT, int MODE, int NG>
+__device__ __forceinline__ void tile_mma_multi(const TileBuf (&b)[NG], const uint8_t* lds, int tstride,
+                                               f32x4_t (&acc)[NG][MT]) {
   const int lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int c = 0; c < kRangeLoads; ++c) {
-    const uint32_t s0 = tile_scale(b0, c), s1 = tile_scale(b1, c);
+    uint32_t sc[NG];
+#pragma unroll
+    for (int i = 0; i < NG; ++i) sc[i] = tile_scale(b[i], c);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const u32x4_t w0 = MODE == 0   ? dq8_bf16_fast(b0.w[c][q], s0)
-                         : MODE == 2 ? dq8_f16_fast(b0.w[c][q], s0)
-                                     : dq8_bf16_exact(b0.w[c][q], s0);
-      const u32x4_t w1 = MODE == 0   ? dq8_bf16_fast(b1.w[c][q], s1)
-                         : MODE == 2 ? dq8_f16_fast(b1.w[c][q], s1)
-                                     : dq8_bf16_exact(b1.w[c][q], s1);
+      u32x4_t w[NG];
+#pragma unroll
+      for (int i = 0; i < NG; ++i)
+        w[i] = MODE == 0   ? dq8_bf16_fast(b[i].w[c][q], sc[i])
+               : MODE == 2 ? dq8_f16_fast(b[i].w[c][q], sc[i])
+                           : dq8_bf16_exact(b[i].w[c][q], sc[i]);
       const int ch = (4 * c + g) * 4 + q;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const u32x4_t xb = *reinterpret_cast<const u32x4_t*>(lds + (16 * mt + n) * tstride + 16 * (ch ^ n));
-        if constexpr (MODE == 2) {
-          acc0[mt] = mfma16x16x32_f16(w0, xb, acc0[mt]);
-          acc1[mt] = mfma16x16x32_f16(w1, xb, acc1[mt]);
-        } else if constexpr (MODE == 3) {
+        if constexpr (MODE == 3) {
           u32x4_t xh, xl;
           f16x8_split_bf16(xb, xh, xl);
-          acc0[mt] = mfma16x16x32(w0, xl, mfma16x16x32(w0, xh, acc0[mt]));
-          acc1[mt] = mfma16x16x32(w1, xl, mfma16x16x32(w1, xh, acc1[mt]));
+#pragma unroll
+          for (int i = 0; i < NG; ++i) acc[i][mt] = mfma16x16x32(w[i], xl, mfma16x16x32(w[i], xh, acc[i][mt]));
         } else {
-          acc0[mt] = mfma16x16x32(w0, xb, acc0[mt]);
-          acc1[mt] = mfma16x16x32(w1, xb, acc1[mt]);
+#pragma unroll
+          for (int i = 0; i < NG; ++i)
+            acc[i][mt] = MODE == 2 ? mfma16x16x32_f16(w[i], xb, acc[i][mt]) : mfma16x16x32(w[i], xb, acc[i][mt]);
         }
       }
       // one quarter at a time: the compiler would otherwise hoist every
@@ -169,24 +169,25 @@ __device__ __forceinline__ void tile_mma_pair(const TileBuf& b0, const TileBuf& 
   }
 }
 
-template <int MT, int DT>
-__device__ __forceinline__ void tile_pair_mma(const TileBuf& b0, const TileBuf& b1, const uint8_t* lds, int tstride,
-                                              f32x4_t (&acc0)[MT], f32x4_t (&acc1)[MT]) {
+template <int MT, int DT, int NG>
+__device__ __forceinline__ void tile_multi_mma(const TileBuf (&b)[NG], const uint8_t* lds, int tstride,
+                                               f32x4_t (&acc)[NG][MT]) {
   bool ok = true;
 #pragma unroll
-  for (int c = 0; c < kRangeLoads; ++c) {
-    ok = ok && (DT == kBF16 ? e8m0_fast_ok(tile_scale(b0, c)) : e8m0_f16_ok(tile_scale(b0, c)));
-    ok = ok && (DT == kBF16 ? e8m0_fast_ok(tile_scale(b1, c)) : e8m0_f16_ok(tile_scale(b1, c)));
-  }
-  if (wave_all(ok)) tile_mma_pair<MT, DT == kBF16 ? 0 : 2>(b0, b1, lds, tstride, acc0, acc1);
-  else tile_mma_pair<MT, DT == kBF16 ? 1 : 3>(b0, b1, lds, tstride, acc0, acc1);
+  for (int c = 0; c < kRangeLoads; ++c)
+#pragma unroll
+    for (int i = 0; i < NG; ++i)
+      ok = ok && (DT == kBF16 ? e8m0_fast_ok(tile_scale(b[i], c)) : e8m0_f16_ok(tile_scale(b[i], c)));
+  if (wave_all(ok)) tile_mma_multi<MT, DT == kBF16 ? 0 : 2, NG>(b, lds, tstride, acc);
+  else tile_mma_multi<MT, DT == kBF16 ? 1 : 3, NG>(b, lds, tstride, acc);
 }
 
-// PAIR: every wave owns exactly two groups (ngroups = 2 * wpk * 8, the 8B down
-// stage at every token count): they are multiplied together, one LDS read
-// of each activation operand for both.  A kernel of its own, so that the
-// loop form's registers are not raised by it.
-template <int MT, int DT, bool PAIR>
+// NG > 0: every wave owns exactly NG groups (ngroups = NG * wpk * 8; 8B down
+// at every token count: 2, 8B gate_up at 17..64 tokens: 3): all of them are
+// loaded at once and multiplied together, one LDS read of each activation
+// operand for all.  Kernels of their own, so that the loop form's (NG = 0)
+// registers are not raised by them.
+template <int MT, int DT, int NG>
 __global__ __launch_bounds__(kTThreads, 1) void tile_kernel(TileArgs a) {
   constexpr int kXPre = MT * 16 * (kRangeK / 8) / kTThreads;   // 16-byte x chunks per thread
   extern __shared__ __align__(16) uint8_t lds[];
@@ -208,10 +209,11 @@ __global__ __launch_bounds__(kTThreads, 1) void tile_kernel(TileArgs a) {
     const int tr = t < a.M ? t : a.M - 1;
     xv[p] = *reinterpret_cast<const u32x4_t*>(a.x + (int64_t)tr * a.K + (int64_t)kr * kRangeK + 8 * (c & 127));
   }
-  TileBuf b0, b1;
+  TileBuf b0, b1, bx;
   auto group_of = [&](int j) { return units > 0 ? slot + (j < units ? j : units - 1) * nslots : slot % a.ngroups; };
   tile_issue(a, group_of(0), kr, b0);
   tile_issue(a, group_of(1), kr, b1);
+  if constexpr (NG == 3) tile_issue(a, group_of(2), kr, bx);
 #pragma unroll
   for (int p = 0; p < kXPre; ++p) {
     const int c = threadIdx.x + p * kTThreads;
@@ -245,14 +247,20 @@ __global__ __launch_bounds__(kTThreads, 1) void tile_kernel(TileArgs a) {
     if constexpr (decltype(issue_tag)::value) tile_issue(a, group_of(j + 2), kr, b);
     store(G, acc);
   };
-  if constexpr (PAIR) {
-    // the wave's whole share is the two groups in flight
-    f32x4_t acc0[MT], acc1[MT];
+  if constexpr (NG > 0) {
+    // the wave's whole share: the groups in b0, b1 and (NG = 3) bx
+    TileBuf bs[NG];
+    bs[0] = b0;
+    bs[1] = b1;
+    if constexpr (NG == 3) bs[2] = bx;
+    f32x4_t acc[NG][MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc0[mt] = acc1[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    tile_pair_mma<MT, DT>(b0, b1, lds, kTokenLds, acc0, acc1);
-    store(group_of(0), acc0);
-    store(group_of(1), acc1);
+    for (int i = 0; i < NG; ++i)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[i][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    tile_multi_mma<MT, DT, NG>(bs, lds, kTokenLds, acc);
+#pragma unroll
+    for (int i = 0; i < NG; ++i) store(group_of(i), acc[i]);
     return;
   }
   constexpr std::true_type kIssue{};
@@ -461,7 +469,10 @@ bool aligned_tile(const void* p, uintptr_t n) { return (reinterpret_cast<uintptr
 template <int MT, int DT>
 hipError_t tile_launch(const TileArgs& a, int grid, hipStream_t st) {
   const int lds = MT * 16 * kTokenLds;
-  auto k = a.ngroups == 2 * a.wpk * kTW ? tile_kernel<MT, DT, true> : tile_kernel<MT, DT, false>;
+  const int nslots = a.wpk * kTW;
+  auto k = a.ngroups == 2 * nslots   ? tile_kernel<MT, DT, 2>
+           : a.ngroups == 3 * nslots ? tile_kernel<MT, DT, 3>
+                                     : tile_kernel<MT, DT, 0>;
   if (lds > 64 * 1024 &&
       hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, lds) !=
           hipSuccess)
