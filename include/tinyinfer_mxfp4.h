@@ -93,10 +93,12 @@ int tinyinfer_mlp_forward_mxfp4(const void* X, const uint8_t* gate, const uint8_
  * Same arguments, kernels and results as tinyinfer_mlp_forward_mxfp4; the
  * split-K partial sums go to a fixed 64 MiB device array of the library (one
  * per device, held until the process ends) instead of an allocated
- * workspace, and no hipMalloc/hipFree is called.  A call whose split-K tile
- * kernels would need more than 64 MiB (far beyond the Qwen3 MLP shapes) is
- * refused with TI_ERR_SCRATCH; the GEMM path splits K only as far as the
- * array holds.  All calls on one device share its array: calls that overlap
+ * workspace, and no hipMalloc/hipFree is called.  A call of up to 64 tokens
+ * whose split-K tile kernels would need more than 64 MiB (far beyond the
+ * Qwen3 MLP shapes) is refused with TI_ERR_SCRATCH; from 65 tokens such a
+ * call runs on the GEMM path instead (kernels, and so bits, may then differ
+ * from tinyinfer_mlp_forward_mxfp4's, within the parity bar); the GEMM path
+ * splits K only as far as the array holds.  All calls on one device share its array: calls that overlap
  * on a device (other streams or threads, concurrent graph replays) race and
  * must not run at the same time.
  */

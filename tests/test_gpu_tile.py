@@ -1,10 +1,10 @@
-"""GPU parity of the split-K tile kernels (9..64 bf16 or fp16 tokens, K a
+"""GPU parity of the split-K tile kernels (9..80 bf16 or fp16 tokens, K a
 multiple of 1024): TI_PATH_SKINNY and TI_PATH_AUTO run them for small batches
 the decode kernels do not take.
 
 Each stage is checked against the CPU oracle with the kernel's rounding
 points (exact fp32 sums, h rounded once), as for the decode kernels.  The
-cases cover one to four 16-token column tiles with a partial last one, one
+cases cover one to five 16-token column tiles with a partial last one, one
 K range (Qwen3-0.6B gate_up) and 25 of them, a grid with fewer row groups
 than waves, scale bytes outside the hardware conversion's exact range (NaN
 included), fp16 activations (fp16 MFMAs, fp16-subnormal weights, and the
@@ -32,7 +32,7 @@ def capi():
     return c
 
 
-@pytest.mark.parametrize("m", [9, 16, 17, 33, 48, 64])
+@pytest.mark.parametrize("m", [9, 16, 17, 33, 48, 64, 72, 80])
 @pytest.mark.parametrize("h,i", [
     (4096, 12288),   # Qwen3-8B: gate_up 4 K ranges, down 12
     (1024, 3072),    # Qwen3-0.6B: gate_up one K range (48 workgroups), down 3

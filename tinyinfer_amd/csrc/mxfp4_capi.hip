@@ -59,12 +59,16 @@ constexpr size_t kGemmMinTokens = 96;
 constexpr size_t kRingMinTokens = 16;
 // Token count up to which the streaming decode kernels are used.
 constexpr size_t kStreamMaxTokens = 8;
-// split-K tile kernels: up to 64 tokens (four 16-token MFMA column tiles)
-constexpr size_t kTileMaxTokens = 64;
+// split-K tile kernels: up to 80 tokens (five 16-token MFMA column tiles)
+constexpr size_t kTileMaxTokens = 80;
+// up to this many tokens a caller-provided workspace too small for the tile
+// kernels' split is refused (TI_ERR_SCRATCH); from 65 tokens such a call
+// takes the ring GEMM, which splits K only as far as the workspace holds
+constexpr size_t kTileScratchTokens = 64;
 
 // One stage of a small batch on the best kernel that takes it: 2..4 tokens on
 // the row-pair kernels, one or two on the row-streaming kernels, n <= 8 on the
-// 8-row item kernels, n <= 64 on the split-K tile kernels, else the
+// 8-row item kernels, n <= 80 on the split-K tile kernels, else the
 // 16-token-tile skinny kernels.  Chosen per stage: the two stages' K differ
 // (at 8B and n = 8 down's activations exceed the LDS the item kernel stages
 // them in, while gate_up's fit).
@@ -91,7 +95,7 @@ int mlp_impl(const MlpArgs& a, int stage, int path, void* stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   // a caller-provided workspace (the no-alloc entry point) must hold the
   // whole split of the tile kernels when they would run
-  if (a.ws && (path == TI_PATH_AUTO || path == TI_PATH_SKINNY) && (size_t)a.n <= kTileMaxTokens &&
+  if (a.ws && (path == TI_PATH_AUTO || path == TI_PATH_SKINNY) && (size_t)a.n <= kTileScratchTokens &&
       tinyinfer::tile_enabled()) {
     size_t need = 0;
     for (int sg : {(int)tinyinfer::kStageGateUp, (int)tinyinfer::kStageDown})

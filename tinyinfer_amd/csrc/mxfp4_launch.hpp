@@ -116,7 +116,7 @@ bool rowpair_enabled();
 bool rowpair_supported(const MlpArgs& a, int stage);
 hipError_t launch_rowpair_mlp(const MlpArgs& a, int stage, hipStream_t stream);
 
-// Split-K tile kernels for up to 64 tokens (K % 1024 == 0): a workgroup
+// Split-K tile kernels for up to 80 tokens (K % 1024 == 0): a workgroup
 // owns one 1024-element K range (its activations staged once in LDS) and
 // streams 16-row weight groups through MFMA; a reduce launch adds the K
 // ranges in order and applies the epilogue (gate_up in one launch, partials

@@ -62,8 +62,9 @@ extern "C" int tinyinfer_mlp_forward_mxfp4_noalloc(const void* X, const uint8_t*
   if (!p) return TI_ERR_HIP;
   a.ws = p;
   a.ws_bytes = kScratchBytes;
-  // run_mlp refuses (TI_ERR_SCRATCH) a call whose tile kernels would need
-  // more than kScratchBytes, rather than allocate or change kernels behind
-  // the caller; the GEMM path splits K only as far as scratch holds
+  // run_mlp refuses (TI_ERR_SCRATCH) a call of up to 64 tokens whose tile
+  // kernels would need more than kScratchBytes, rather than allocate or
+  // change kernels behind the caller (from 65 tokens such a call takes the
+  // GEMM path); the GEMM path splits K only as far as scratch holds
   return tinyinfer::run_mlp(a, tinyinfer::kStageBoth, TI_PATH_AUTO, stream);
 }

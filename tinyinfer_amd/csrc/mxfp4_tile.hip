@@ -1,4 +1,4 @@
-// Split-K tile kernels for small batches (up to 64 bf16 or fp16 tokens): the
+// Split-K tile kernels for small batches (up to 80 bf16 or fp16 tokens): the
 // reference's per-token GEMV stages mlp_stage1_mxfp4 / mlp_stage2_mxfp4
 // (tinyinfer/csrc/mlp_fp4.cu:79-142, 365-426) for a batch whose activations
 // are too many for the decode kernels' registers (or whose K they decline,
@@ -35,6 +35,7 @@ constexpr int kTThreads = kTW * 64;
 constexpr int kRangeK = 1024;              // K elements per workgroup range
 constexpr int kRangeLoads = kRangeK / 128; // 16-byte loads per lane per group (16 rows x 64 B each)
 constexpr int kTokenLds = kRangeK * 2;     // LDS bytes per token of the range
+constexpr int kTileMaxM = 80;              // five 16-token column tiles: 160 KB of activations in LDS
 
 struct TileArgs {
   const uint16_t* x;       // [M, K]
@@ -442,7 +443,7 @@ int tile_cus() { return device_info().cus; }
 // groups per wave; 12.4 -> 12.1 us).
 bool tile_plan(int64_t M, int64_t K, int64_t R, bool gateup, TileArgs& a, int& grid, int& mt, size_t& ws_bytes) {
   const int cus = tile_cus();
-  if (cus < 1 || M < 1 || M > 64 || K < kRangeK || K % kRangeK != 0 || K > (1 << 20) || R < 16 || R % 16 != 0 ||
+  if (cus < 1 || M < 1 || M > kTileMaxM || K < kRangeK || K % kRangeK != 0 || K > (1 << 20) || R < 16 || R % 16 != 0 ||
       R > (1 << 22))
     return false;
   mt = (int)((M + 15) / 16);
@@ -540,6 +541,7 @@ hipError_t tile_stage(const MlpArgs& m, hipStream_t st) {
     case 2: e = tile_launch<2, DT>(a, grid, st); break;
     case 3: e = tile_launch<3, DT>(a, grid, st); break;
     case 4: e = tile_launch<4, DT>(a, grid, st); break;
+    case 5: e = tile_launch<5, DT>(a, grid, st); break;
     default: break;
   }
   if (e != hipSuccess) return e;
