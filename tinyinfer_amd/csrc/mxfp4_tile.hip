@@ -334,7 +334,12 @@ __global__ __launch_bounds__(256) void tile_reduce(const float* __restrict__ ws,
 // in order, applies SiLU * up and stores h: no workspace round trip and no
 // reduce launch.  Every wave runs the same iterations (the barrier); blocks
 // past the end repeat the last one and store to `dummy` instead.
-template <int MT, int S, int DT>
+// NI = 3: every workgroup runs exactly three iterations (8B at up to 16
+// tokens: 768 row blocks over 256 workgroups).  Each wave then loads its
+// three groups at once (same K range, so each activation operand read from
+// LDS feeds all three), and the three iterations' partial tiles meet in LDS
+// behind one barrier instead of three.  NI = 0: the loop.
+template <int MT, int S, int DT, int NI>
 __global__ __launch_bounds__(kTThreads, 1) void tile_gu_kernel(TileArgs a, uint16_t* out, uint16_t* dummy) {
   static_assert(S == 1 || S == 2 || S == 4, "8 waves = (4 / S) blocks x 2 matrices x S ranges");
   constexpr int kBlocks = 4 / S;
@@ -382,22 +387,9 @@ __global__ __launch_bounds__(kTThreads, 1) void tile_gu_kernel(TileArgs a, uint1
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 
-  auto step = [&](TileBuf& b, int it, auto issue_tag) __attribute__((always_inline)) {
-    f32x4_t acc[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    tile_group_mma<MT, DT>(b, lds + sp * kTokenLds, tstride, acc);
-    if constexpr (decltype(issue_tag)::value) tile_issue(a, mat * nrb + rb_of(it + 2), sp, b);
-    float* pw = part + ((it & 1) * kTW + wave) * MT * 256;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) *reinterpret_cast<f32x4_t*>(pw + (mt * 64 + lane) * 4) = acc[mt];
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    // outputs o = (block, token, row): row fastest, so a token's 16 rows are
-    // one 32-byte store run
-    const float* pr = part + (it & 1) * kTW * MT * 256;
+  // iteration it's outputs from its partial tiles at pr: o = (block, token,
+  // row), row fastest, so a token's 16 rows are one 32-byte store run
+  auto emit = [&](int it, const float* pr) __attribute__((always_inline)) {
 #pragma unroll
     for (int k = 0; k < kOutTrips; ++k) {
       const int o = kOut >= kTThreads ? (int)threadIdx.x + k * kTThreads : (int)threadIdx.x % kOut;
@@ -414,6 +406,46 @@ __global__ __launch_bounds__(kTThreads, 1) void tile_gu_kernel(TileArgs a, uint1
       uint16_t* dst = valid ? out + (int64_t)t * a.R + rb * 16 + i : dummy + threadIdx.x;
       *dst = f32_to_act<DT>(silu_f32(g) * u);
     }
+  };
+  if constexpr (NI == 3) {
+    TileBuf bs[3];
+    bs[0] = b0;
+    bs[1] = b1;
+    tile_issue(a, mat * nrb + rb_of(2), sp, bs[2]);   // after x left the registers
+    f32x4_t acc[3][MT];
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[j][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    tile_multi_mma<MT, DT, 3>(bs, lds + sp * kTokenLds, tstride, acc);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      float* pw = part + (j * kTW + wave) * MT * 256;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) *reinterpret_cast<f32x4_t*>(pw + (mt * 64 + lane) * 4) = acc[j][mt];
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int j = 0; j < 3; ++j) emit(j, part + j * kTW * MT * 256);
+    return;
+  }
+  auto step = [&](TileBuf& b, int it, auto issue_tag) __attribute__((always_inline)) {
+    f32x4_t acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    tile_group_mma<MT, DT>(b, lds + sp * kTokenLds, tstride, acc);
+    if constexpr (decltype(issue_tag)::value) tile_issue(a, mat * nrb + rb_of(it + 2), sp, b);
+    float* pw = part + ((it & 1) * kTW + wave) * MT * 256;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) *reinterpret_cast<f32x4_t*>(pw + (mt * 64 + lane) * 4) = acc[mt];
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    emit(it, part + (it & 1) * kTW * MT * 256);
   };
   constexpr std::true_type kIssue{};
   constexpr std::false_type kLast{};
@@ -493,14 +525,20 @@ bool tile_gu_enabled() { return option(kOptTileGu) != 0; }
 
 template <int MT, int S, int DT>
 hipError_t tile_gu_launch(const TileArgs& a, int grid, uint16_t* out, hipStream_t st) {
-  const int lds = 16 * MT * S * kTokenLds + 2 * kTW * MT * 256 * (int)sizeof(float);
-  auto k = tile_gu_kernel<MT, S, DT>;
-  if (lds > 64 * 1024 &&
-      hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, lds) !=
+  const int nrb = a.R / 16;
+  const int niter = (nrb + grid * (4 / S) - 1) / (grid * (4 / S));
+  // three iterations' partial tiles at once when each workgroup runs three
+  const int part_tile = kTW * MT * 256 * (int)sizeof(float);
+  const int lds3 = 16 * MT * S * kTokenLds + 3 * part_tile;
+  const bool three = niter == 3 && lds3 <= device_info().lds_per_block;
+  auto k = three ? tile_gu_kernel<MT, S, DT, 3> : tile_gu_kernel<MT, S, DT, 0>;
+  const int lds_k = three ? lds3 : 16 * MT * S * kTokenLds + 2 * part_tile;
+  if (lds_k > 64 * 1024 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, lds_k) !=
           hipSuccess)
     return hipErrorNotSupported;
   // stores of outputs past the end go to the (otherwise unused) workspace
-  hipLaunchKernelGGL(k, dim3(grid), dim3(kTThreads), (size_t)lds, st, a, out, reinterpret_cast<uint16_t*>(a.ws));
+  hipLaunchKernelGGL(k, dim3(grid), dim3(kTThreads), (size_t)lds_k, st, a, out, reinterpret_cast<uint16_t*>(a.ws));
   return hipGetLastError();
 }
 
